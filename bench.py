@@ -1,0 +1,259 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused attention operator on one MI355X.
+
+A step is one simulated DiT denoising step of the batch-64 throughput sweep: 14 blocks x
+(self-attention 64 x 9 heads x 256 x 64, then cross-attention with per-sequence key lengths
+~ U{1..128}), each block with its own device-resident inputs. `value` is the whole sweep's
+sustained fp32 TFLOP/s (FLOPs = 4*D per attended query/key pair, app/gpu/ops.js:116).
+
+The same JSON line carries:
+  headline     DiT self-attention batch 2 x 9 x 256 x 64: us/call, TFLOP/s, fraction of peak
+  per_config   us/call and TFLOP/s of the other single-call configs (DiT cross, T5, VAE)
+  roofline     the dominant kernel (sweep self-attention), timed per launch with HIP events
+  cpu_baseline the PyTorch fp32 CPU formulation of tools/reference.py:72-79 on a bounded sample
+
+    python bench.py [--steps 50] [--warmup 3] [--cpu-steps 4] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "supra2-img-web_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "fused-attn µs/call + TFLOP/s (DiT 2×9×256×64 fp32), % of fp32 MFMA peak"
+PEAK_TFLOPS = 157.3  # MI355X dense fp32 MFMA
+PEAK_HBM_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    sys.stderr.write(f"[bench {time.strftime('%H:%M:%S')}] {msg}\n")
+    sys.stderr.flush()
+
+
+def time_calls(dev, launch, n: int, warmup: int) -> float:
+    """Average ms per call of `launch` over n back-to-back calls on the device stream."""
+    from supra_attn.device import Event
+
+    for _ in range(warmup):
+        launch()
+    dev.sync()
+    e0, e1 = Event(), Event()
+    e0.record(dev.stream)
+    for _ in range(n):
+        launch()
+    e1.record(dev.stream)
+    dev.sync()
+    return e0.elapsed_ms(e1) / n
+
+
+def traffic_from_profiles(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summary, if any."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(kernel, {}).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(data, steps: int) -> dict:
+    """PyTorch fp32 CPU on `steps` full sweep steps (28 calls each), the tools/reference.py
+    formulation, inputs already in host memory."""
+    import torch
+
+    from oracle import attention as orc
+
+    threads = torch.get_num_threads()
+    blocks = [data.block(i) for i in range(data.blocks)]
+    flops = sum(s.flops() + c.flops() for s, c in blocks)
+    # warm-up call
+    orc.cpu_dit_self(blocks[0][0])
+    t0 = time.perf_counter()
+    for st in range(steps):
+        for s, c in blocks:
+            orc.cpu_dit_self(s)
+            orc.cpu_dit_cross(c)
+        log(f"cpu baseline step {st + 1}/{steps} done")
+    dt = time.perf_counter() - t0
+    return {
+        "value": flops * steps / dt / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{steps} of the sweep's denoising steps ({28 * steps} calls: 14 blocks x self+cross, batch 64) "
+                  f"with torch {torch.__version__} F.scaled_dot_product_attention on the CPU "
+                  f"({os.cpu_count()} logical CPUs visible, {threads} threads, {platform.processor() or platform.machine()}); "
+                  f"{dt:.2f} s, {dt / steps * 1e3:.1f} ms/step",
+        "ms_per_step": dt / steps * 1e3,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--cpu-steps", type=int, default=4)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calls", type=int, default=200, help="calls per single-config timing")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this operator's path has no multi-GPU form here (asked for --gpus {args.gpus}); "
+              "the per-GPU shard of a sharded run is the same kernel at the shapes measured with --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    from supra_attn import workloads
+    from supra_attn.device import Device, Event
+    from supra_attn.runner import Staged
+
+    dev = Device(0)
+    log("generating sweep inputs")
+    data = workloads.SweepData()
+    staged = []
+    for i in range(data.blocks):
+        s, c = data.block(i)
+        staged.append((Staged(dev, s), Staged(dev, c)))
+    dev.sync()
+    self_kernel = staged[0][0].kernel
+    cross_kernel = staged[0][1].kernel
+    step_flops = sum(s.call.flops() + c.call.flops() for s, c in staged)
+    log(f"sweep staged: {data.blocks} blocks, self={self_kernel}, cross={cross_kernel}, "
+        f"{step_flops / 1e9:.2f} GFLOP/step")
+
+    def step():
+        for s, c in staged:
+            s.launch()
+            c.launch()
+
+    for _ in range(args.warmup):
+        step()
+    dev.sync()
+    e0, e1 = Event(), Event()
+    e0.record(dev.stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(dev.stream)
+    dev.sync()
+    total_ms = e0.elapsed_ms(e1)
+    ms_per_step = total_ms / args.steps
+    value = step_flops * args.steps / (total_ms * 1e-3) / 1e12
+    log(f"sweep: {ms_per_step:.3f} ms/step, {value:.2f} TFLOP/s")
+
+    # per-launch timing of each kernel over the same sweep (separate instrumented pass)
+    pairs_s = [(Event(), Event()) for _ in range(args.steps * data.blocks)]
+    pairs_c = [(Event(), Event()) for _ in range(args.steps * data.blocks)]
+    n = 0
+    for _ in range(args.steps):
+        for s, c in staged:
+            a, b = pairs_s[n]
+            a.record(dev.stream)
+            s.launch()
+            b.record(dev.stream)
+            a, b = pairs_c[n]
+            a.record(dev.stream)
+            c.launch()
+            b.record(dev.stream)
+            n += 1
+    dev.sync()
+    self_ms = sum(a.elapsed_ms(b) for a, b in pairs_s) / len(pairs_s)
+    cross_ms = sum(a.elapsed_ms(b) for a, b in pairs_c) / len(pairs_c)
+    self_call = staged[0][0].call
+    self_flops = self_call.flops()
+    achieved = self_flops / (self_ms * 1e-3) / 1e12
+    cross_flops = sum(c.call.flops() for _, c in staged) / len(staged)
+    log(f"per launch: self {self_ms * 1e3:.1f} us ({achieved:.1f} TFLOP/s), cross {cross_ms * 1e3:.1f} us")
+
+    # single-call configs
+    per_config = {}
+    for name, make in workloads.CONFIGS.items():
+        call = make()
+        st = Staged(dev, call)
+        ms = time_calls(dev, st.launch, args.calls, warmup=10)
+        tf = call.flops() / (ms * 1e-3) / 1e12
+        per_config[name] = {
+            "kernel": st.kernel,
+            "us_per_call": ms * 1e3,
+            "tflops": tf,
+            "frac_peak": tf / PEAK_TFLOPS,
+            "gbs": call.algorithmic_bytes() / (ms * 1e-3) / 1e9,
+            "flops_per_call": call.flops(),
+            "bytes_per_call": call.algorithmic_bytes(),
+        }
+        st.release()
+        log(f"{name}: {ms * 1e3:.2f} us/call, {tf:.2f} TFLOP/s via {per_config[name]['kernel']}")
+    for s, c in staged:
+        s.release()
+        c.release()
+
+    cpu = None
+    if not args.no_cpu:
+        log(f"cpu baseline: {args.cpu_steps} steps")
+        cpu = cpu_baseline(data, args.cpu_steps)
+        log(f"cpu baseline: {cpu['value']:.4f} TFLOP/s")
+
+    head = per_config["dit_self_b2"]
+    result = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: seeded N(0,1) inputs, 14 distinct device-resident input sets",
+        "config": {
+            "workload": "dit_sweep_b64: 14 blocks x (self 64x9x256x64 + cross 64x9x256x64, key_len~U{1..128}) per step",
+            "global_batch": 64,
+            "seq_len": 256,
+            "heads": 9,
+            "head_dim": 64,
+            "cross_key_len_sum": int(data.key_len.sum()),
+            "gflop_per_step": round(step_flops / 1e9, 4),
+            "frac_peak": round(value / PEAK_TFLOPS, 4),
+            "parallelism": "single GPU",
+        },
+        "headline": {
+            "workload": "dit_self_b2 (2x9x256x64)",
+            "us_per_call": round(head["us_per_call"], 3),
+            "tflops": round(head["tflops"], 3),
+            "frac_peak": round(head["frac_peak"], 4),
+        },
+        "roofline": {
+            "kernel": self_kernel,
+            "bound": "mfma",
+            "achieved": round(achieved, 3),
+            "peak": PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_TFLOPS, 4),
+            "traffic": traffic_from_profiles(self_kernel),
+            "algorithmic_flops_per_launch": self_flops,
+            "algorithmic_bytes_per_launch": self_call.algorithmic_bytes(),
+            "us_per_launch": round(self_ms * 1e3, 3),
+            "cross_us_per_launch": round(cross_ms * 1e3, 3),
+            "cross_tflops": round(cross_flops / (cross_ms * 1e-3) / 1e12, 3),
+        },
+        "per_config": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                       for k, v in per_config.items()},
+        "cpu_baseline": None if cpu is None else {k: (round(v, 6) if isinstance(v, float) else v) for k, v in cpu.items()},
+    }
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

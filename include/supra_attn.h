@@ -1,0 +1,149 @@
+/*
+ * supra_attn.h - C ABI of the MI355X (gfx950) fused attention operator.
+ *
+ * This library replaces the attention hot path of Supra2-Img Web: the JS operator
+ * `attention(gpu, {q, k, v, Lq, Lk, H, D, ldq, ldk, ldv, qOff, kOff, vOff, oOff, scale, bias, out})`
+ * (app/gpu/ops.js:103-149), its fused WGSL kernel (app/gpu/kernels.js:164-316), and the unfused
+ * QK^T GEMM -> softmax(+bias) -> PV GEMM chain it falls back to (app/gpu/ops.js:119-147,
+ * app/gpu/kernels.js:27-63, app/gpu/gemm.js:116-223). The device-buffer helpers replace the parts
+ * of the WebGPU runtime that the operator's callers touch (app/gpu/device.js:41-55, 144-191,
+ * 255-269).
+ *
+ * Conventions
+ *  - Every pointer argument named q/k/v/o/bias/key_len/key_mask is a DEVICE pointer.
+ *  - Offsets and strides are in ELEMENTS (floats for q/k/v/o/bias), as in app/gpu/ops.js.
+ *  - All calls are stream-ordered and asynchronous unless documented otherwise; `stream` is a
+ *    hipStream_t passed as void* (NULL = the null stream). Nothing in the attention call
+ *    allocates device memory.
+ *  - Status codes: SA_OK (0) or a negative SA_ERR_* value. A failed call launches nothing.
+ *    sa_last_error() returns a thread-local message describing the last failure.
+ *  - q, k and v may alias one another (the DiT passes one packed qkv buffer as all three,
+ *    app/models/dit.js:172). o must not overlap any of them.
+ */
+#ifndef SUPRA_ATTN_H
+#define SUPRA_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SA_ABI_VERSION 1
+
+/* ---- status codes ---- */
+#define SA_OK 0
+#define SA_ERR_INVALID (-1)     /* invalid argument (null pointer, non-positive size, bad stride) */
+#define SA_ERR_UNSUPPORTED (-2) /* a valid request outside what this build implements */
+#define SA_ERR_HIP (-3)         /* the HIP runtime reported an error */
+#define SA_ERR_ALIAS (-4)       /* the output overlaps an input */
+
+/* ---- additive score bias ---- */
+#define SA_BIAS_NONE 0
+/* Dense bias, element (b, h, i, j) at bias[b*sbias + (h*Lq + i)*Lk + j]: the [H, Lq, Lk] layout
+ * that app/models/t5.js:55-65 builds and app/gpu/kernels.js:34 adds (sbias = 0 shares one bias
+ * across the batch). */
+#define SA_BIAS_DENSE 1
+/* Relative-position bias gathered in-kernel (HF T5 compute_bias, mirrored by
+ * app/models/t5.js:55-65): element (b, h, i, j) = bias[bucket_lut[j - i + Lq - 1] * H + h], with
+ * bias the [num_buckets, H] table of app/models/t5.js:44 and bucket_lut an int32 device array of
+ * Lq + Lk - 1 buckets (fill it with sa_t5_bucket_lut). */
+#define SA_BIAS_RELPOS 2
+
+/* ---- key masking (on top of the Lk bound) ---- */
+#define SA_MASK_NONE 0
+/* Per-sequence key length: keys j >= key_len[b] are masked (0 <= key_len[b] <= Lk). This is the
+ * padded form of app/models/dit.js:182-185, which runs each sample at its own Lk. */
+#define SA_MASK_KEY_LEN 1
+/* Boolean key-padding mask, key_mask[b*smask + j] != 0 means "attend": the
+ * F.scaled_dot_product_attention boolean convention of tools/reference.py:78. */
+#define SA_MASK_KEY_MASK 2
+
+/*
+ * Arguments of one attention call: for every sequence b < B, head h < H and query i < Lq,
+ *
+ *   s_ij   = scale * sum_d Q[b,i,h,d] K[b,j,h,d] + bias(b,h,i,j)
+ *   O[b,i,h,:] = sum_{j attended} softmax_j(s_ij) V[b,j,h,:]
+ *
+ * with Q[b,i,h,d] = q[q_off + b*sq + i*ldq + h*D + d] (likewise k, v, o). A query row whose keys
+ * are all masked produces zeros (the F.scaled_dot_product_attention convention).
+ *
+ * Set struct_size = sizeof(sa_attn_args) (checked, so that later ABI revisions can grow the
+ * struct). Zero-initialise unused fields.
+ */
+typedef struct sa_attn_args {
+  uint32_t struct_size;
+  int32_t B;  /* sequences in the batch (app/models/dit.js loops these on the host) */
+  int32_t H;  /* heads */
+  int32_t D;  /* head dim */
+  int32_t Lq; /* queries per sequence */
+  int32_t Lk; /* keys per sequence (the padded length when a mask is used) */
+  const float* q;
+  const float* k;
+  const float* v;
+  float* o;
+  int64_t q_off, k_off, v_off, o_off; /* element offsets (qOff/kOff/vOff/oOff in ops.js) */
+  int64_t ldq, ldk, ldv, ldo;         /* row strides; ldo <= 0 means H*D (ops.js:114) */
+  int64_t sq, sk, sv, so;             /* batch strides; ignored when B == 1 */
+  float scale;                        /* softmax scale; the JS default 1/sqrt(D) is set by callers */
+  int32_t bias_mode;                  /* SA_BIAS_* */
+  const float* bias;                  /* DENSE: [B?][H, Lq, Lk]; RELPOS: table [num_buckets, H] */
+  int64_t sbias;                      /* DENSE batch stride in elements (0 = shared) */
+  const int32_t* bucket_lut;          /* RELPOS: Lq + Lk - 1 bucket ids, index j - i + Lq - 1 */
+  int32_t num_buckets;                /* RELPOS: rows of the table */
+  int32_t mask_mode;                  /* SA_MASK_* */
+  const int32_t* key_len;             /* KEY_LEN: [B] */
+  const uint8_t* key_mask;            /* KEY_MASK: [B, smask] */
+  int64_t smask;                      /* KEY_MASK batch stride (bytes = elements); <= 0 means Lk */
+} sa_attn_args;
+
+/* Fused attention, fp32 in and out, fp32 MFMA arithmetic. Replaces ops.attention
+ * (app/gpu/ops.js:103-149) for every caller in app/models/{dit,t5,vae}.js; B folds the
+ * per-sample host loops of app/models/dit.js:170-185 into one launch. Asynchronous on `stream`. */
+int sa_attention_f32(const sa_attn_args* args, void* stream);
+
+/* Which kernel sa_attention_f32 would launch for these arguments (a static name such as
+ * "flash_mfma_d64"), or NULL with sa_last_error() set if the arguments are rejected. Host only. */
+const char* sa_attention_kernel_name(const sa_attn_args* args);
+
+/* T5 bidirectional/unidirectional relative-position bucket of each relative position
+ * rel = j - i for j in [0, Lk), i in [0, Lq): out[rel + Lq - 1] for the Lq + Lk - 1 values of rel.
+ * Follows HF T5Attention._relative_position_bucket in float32, as app/models/t5.js:14-23 does.
+ * Host memory, synchronous. */
+int sa_t5_bucket_lut(int32_t Lq, int32_t Lk, int32_t num_buckets, int32_t max_distance,
+                     int32_t bidirectional, int32_t* out);
+
+/* Dense [H, Lq, Lk] bias from a [num_buckets, H] table and a bucket LUT, written to device memory
+ * `out` (app/models/t5.js:55-65, for callers that pass a dense bias). Asynchronous on `stream`. */
+int sa_t5_position_bias(const float* table, const int32_t* bucket_lut, int32_t num_buckets, int32_t H,
+                        int32_t Lq, int32_t Lk, float* out, void* stream);
+
+/* ---- device runtime helpers (app/gpu/device.js: GPU.empty/fromArray/upload/read/sync) ---- */
+int sa_device_count(int32_t* count);
+int sa_set_device(int32_t device);
+int sa_malloc(void** ptr, size_t bytes);   /* device memory; synchronous */
+int sa_free(void* ptr);                    /* synchronous (waits for the device) */
+int sa_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream); /* stream-ordered */
+int sa_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream); /* waits for stream */
+int sa_memset(void* dst, int value, size_t bytes, void* stream);
+int sa_stream_create(void** stream);       /* a non-blocking stream at the default priority */
+int sa_stream_destroy(void* stream);
+int sa_stream_sync(void* stream);          /* the JS shim's gpu.sync() */
+int sa_device_sync(void);
+
+/* ---- timing (the timestamp profiler of app/gpu/device.js:272-325) ---- */
+int sa_event_create(void** event);
+int sa_event_destroy(void* event);
+int sa_event_record(void* event, void* stream);
+int sa_event_elapsed_ms(float* ms, void* start, void* stop); /* waits for stop */
+
+/* ---- diagnostics ---- */
+int sa_version(void);             /* SA_ABI_VERSION */
+const char* sa_last_error(void);  /* thread-local; "" when the last call succeeded */
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SUPRA_ATTN_H */

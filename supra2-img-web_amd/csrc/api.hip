@@ -1,0 +1,369 @@
+// C ABI of the attention operator: argument validation, kernel selection and the device-runtime
+// helpers the JS addon and the Python bindings use.
+//
+// The operator contract follows app/gpu/ops.js:103-149 (offsets/strides in floats, default output
+// row stride H*D, synchronous error for an unsupported request) extended with batch strides, a
+// per-sequence key length or boolean key mask, and an in-kernel relative-position bias.
+
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "../../include/supra_attn.h"
+#include "common.h"
+#include "kernels.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return SA_OK;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(SA_ERR_HIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+// Byte extent [lo, hi) touched by a strided [B, L, H*D] view of `base`.
+struct Extent {
+  uintptr_t lo, hi;
+};
+
+Extent extent(const void* base, int64_t off, int64_t sb, int64_t ld, int B, int L, int64_t row) {
+  const int64_t last = off + (B > 1 ? (int64_t)(B - 1) * sb : 0) + (int64_t)(L - 1) * ld + row;
+  return {(uintptr_t)base + (uintptr_t)(off * 4), (uintptr_t)base + (uintptr_t)(last * 4)};
+}
+
+bool overlaps(const Extent& a, const Extent& b) { return a.lo < b.hi && b.lo < a.hi; }
+
+bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+
+// Resolves an sa_attn_args into kernel parameters; returns SA_OK or an error (message set).
+int resolve(const sa_attn_args* a, sa::AttnParams* p) {
+  if (a == nullptr) return fail(SA_ERR_INVALID, "args is NULL");
+  if (a->struct_size != sizeof(sa_attn_args))
+    return fail(SA_ERR_INVALID, "struct_size %u does not match sizeof(sa_attn_args) = %zu", a->struct_size,
+                sizeof(sa_attn_args));
+  if (a->B < 1 || a->H < 1 || a->D < 1 || a->Lq < 1 || a->Lk < 1)
+    return fail(SA_ERR_INVALID, "B, H, D, Lq, Lk must be >= 1 (got B=%d H=%d D=%d Lq=%d Lk=%d)", a->B, a->H, a->D,
+                a->Lq, a->Lk);
+  if (!a->q || !a->k || !a->v || !a->o) return fail(SA_ERR_INVALID, "q, k, v and o must be non-NULL");
+  if (!(isfinite(a->scale))) return fail(SA_ERR_INVALID, "scale must be finite");
+  const int64_t HD = (int64_t)a->H * a->D;
+  const int64_t ldo = a->ldo > 0 ? a->ldo : HD;
+  if (a->q_off < 0 || a->k_off < 0 || a->v_off < 0 || a->o_off < 0)
+    return fail(SA_ERR_INVALID, "offsets must be >= 0");
+  if (a->ldq < HD || a->ldk < HD || a->ldv < HD || ldo < HD)
+    return fail(SA_ERR_INVALID, "row strides must be >= H*D = %lld (ldq=%lld ldk=%lld ldv=%lld ldo=%lld)",
+                (long long)HD, (long long)a->ldq, (long long)a->ldk, (long long)a->ldv, (long long)ldo);
+  if (a->B > 1 && (a->sq < 0 || a->sk < 0 || a->sv < 0 || a->so < 0))
+    return fail(SA_ERR_INVALID, "batch strides must be >= 0");
+  const int64_t so = a->B > 1 ? a->so : 0;
+  if (a->B > 1 && so < (int64_t)(a->Lq - 1) * ldo + HD)
+    return fail(SA_ERR_INVALID, "output batch stride %lld makes sequences overlap", (long long)so);
+
+  // o must not overlap q, k or v (WebGPU forbids binding one buffer as read and read_write in one
+  // dispatch, so the reference never does this either).
+  const Extent eo = extent(a->o, a->o_off, so, ldo, a->B, a->Lq, HD);
+  const Extent eq = extent(a->q, a->q_off, a->sq, a->ldq, a->B, a->Lq, HD);
+  const Extent ek = extent(a->k, a->k_off, a->sk, a->ldk, a->B, a->Lk, HD);
+  const Extent ev = extent(a->v, a->v_off, a->sv, a->ldv, a->B, a->Lk, HD);
+  if (overlaps(eo, eq) || overlaps(eo, ek) || overlaps(eo, ev))
+    return fail(SA_ERR_ALIAS, "the output overlaps q, k or v");
+
+  switch (a->bias_mode) {
+    case SA_BIAS_NONE:
+      break;
+    case SA_BIAS_DENSE:
+      if (!a->bias) return fail(SA_ERR_INVALID, "SA_BIAS_DENSE needs bias");
+      if (a->B > 1 && a->sbias < 0) return fail(SA_ERR_INVALID, "sbias must be >= 0");
+      break;
+    case SA_BIAS_RELPOS:
+      if (!a->bias || !a->bucket_lut) return fail(SA_ERR_INVALID, "SA_BIAS_RELPOS needs bias (table) and bucket_lut");
+      if (a->num_buckets < 1) return fail(SA_ERR_INVALID, "SA_BIAS_RELPOS needs num_buckets >= 1");
+      break;
+    default:
+      return fail(SA_ERR_INVALID, "unknown bias_mode %d", a->bias_mode);
+  }
+  switch (a->mask_mode) {
+    case SA_MASK_NONE:
+      break;
+    case SA_MASK_KEY_LEN:
+      if (!a->key_len) return fail(SA_ERR_INVALID, "SA_MASK_KEY_LEN needs key_len");
+      break;
+    case SA_MASK_KEY_MASK:
+      if (!a->key_mask) return fail(SA_ERR_INVALID, "SA_MASK_KEY_MASK needs key_mask");
+      if (a->B > 1 && a->smask > 0 && a->smask < a->Lk)
+        return fail(SA_ERR_INVALID, "smask %lld is smaller than Lk", (long long)a->smask);
+      break;
+    default:
+      return fail(SA_ERR_INVALID, "unknown mask_mode %d", a->mask_mode);
+  }
+
+  p->q = a->q;
+  p->k = a->k;
+  p->v = a->v;
+  p->o = a->o;
+  p->q_off = a->q_off;
+  p->k_off = a->k_off;
+  p->v_off = a->v_off;
+  p->o_off = a->o_off;
+  p->ldq = a->ldq;
+  p->ldk = a->ldk;
+  p->ldv = a->ldv;
+  p->ldo = ldo;
+  p->sq = a->B > 1 ? a->sq : 0;
+  p->sk = a->B > 1 ? a->sk : 0;
+  p->sv = a->B > 1 ? a->sv : 0;
+  p->so = so;
+  p->B = a->B;
+  p->H = a->H;
+  p->D = a->D;
+  p->Lq = a->Lq;
+  p->Lk = a->Lk;
+  p->scale_log2 = a->scale * sa::kLog2e;
+  p->bias_mode = a->bias_mode;
+  p->bias = a->bias;
+  p->sbias = a->B > 1 ? a->sbias : 0;
+  p->lut = a->bucket_lut;
+  p->num_buckets = a->num_buckets;
+  p->mask_mode = a->mask_mode;
+  p->key_len = a->key_len;
+  p->key_mask = a->key_mask;
+  p->smask = a->B > 1 ? (a->smask > 0 ? a->smask : a->Lk) : 0;
+  return SA_OK;
+}
+
+enum class Path { kFlash, kGeneric };
+
+struct Choice {
+  Path path;
+  int nsplit;
+  const char* name;
+};
+
+// Kernel selection. The MFMA kernels need D in {64, 128} and 16-byte aligned rows (the same gate
+// as the fused path of app/gpu/ops.js:111-112); everything else goes to the generic kernel.
+int choose(const sa::AttnParams& p, Choice* c) {
+  const bool vec = aligned16(p.q) && aligned16(p.k) && aligned16(p.v) && aligned16(p.o) && p.q_off % 4 == 0 &&
+                   p.k_off % 4 == 0 && p.v_off % 4 == 0 && p.o_off % 4 == 0 && p.ldq % 4 == 0 && p.ldk % 4 == 0 &&
+                   p.ldv % 4 == 0 && p.ldo % 4 == 0 && p.sq % 4 == 0 && p.sk % 4 == 0 && p.sv % 4 == 0 &&
+                   p.so % 4 == 0;
+  if ((p.D == 64 || p.D == 128) && vec) {
+    // Units of 32 queries; below ~2 waves per SIMD (256 CUs x 4 SIMDs) split the key blocks
+    // across the waves of a workgroup so that more SIMDs get work.
+    const int64_t units = (int64_t)p.B * p.H * ((p.Lq + 31) / 32);
+    const int nblk = (p.Lk + 31) / 32;
+    int nsplit = 1;
+    if (units < 2048 && nblk >= 2) nsplit = 2;
+    if (units < 1024 && nblk >= 4 && p.D == 64) nsplit = 4;
+    c->path = Path::kFlash;
+    c->nsplit = nsplit;
+    c->name = sa::flash_mfma_name(p.D, nsplit);
+    return SA_OK;
+  }
+  if (p.D > sa::GENERIC_MAX_D)
+    return fail(SA_ERR_UNSUPPORTED, "head dim %d exceeds the supported maximum %d", p.D, sa::GENERIC_MAX_D);
+  c->path = Path::kGeneric;
+  c->nsplit = 1;
+  c->name = "generic";
+  return SA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sa_attention_f32(const sa_attn_args* args, void* stream) {
+  sa::AttnParams p;
+  int rc = resolve(args, &p);
+  if (rc != SA_OK) return rc;
+  Choice c;
+  rc = choose(p, &c);
+  if (rc != SA_OK) return rc;
+  hipError_t e = c.path == Path::kFlash ? sa::launch_flash_mfma(p, c.nsplit, (hipStream_t)stream)
+                                        : sa::launch_generic(p, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, c.name);
+  return ok();
+}
+
+const char* sa_attention_kernel_name(const sa_attn_args* args) {
+  sa::AttnParams p;
+  if (resolve(args, &p) != SA_OK) return nullptr;
+  Choice c;
+  if (choose(p, &c) != SA_OK) return nullptr;
+  ok();
+  return c.name;
+}
+
+int sa_t5_bucket_lut(int32_t Lq, int32_t Lk, int32_t num_buckets, int32_t max_distance, int32_t bidirectional,
+                     int32_t* out) {
+  if (Lq < 1 || Lk < 1 || !out) return fail(SA_ERR_INVALID, "Lq, Lk must be >= 1 and out non-NULL");
+  if (num_buckets < (bidirectional ? 4 : 2) || max_distance < 1)
+    return fail(SA_ERR_INVALID, "num_buckets %d / max_distance %d out of range", num_buckets, max_distance);
+  int nb = num_buckets;
+  if (bidirectional) nb /= 2;
+  const int max_exact = nb / 2;
+  if (max_exact < 1 || max_distance <= max_exact)
+    return fail(SA_ERR_INVALID, "max_distance must exceed num_buckets/%d", bidirectional ? 4 : 2);
+  // float32 arithmetic as torch does it; log is rounded once from double (a correctly rounded
+  // float32 log, like Math.fround(Math.log(x)) in app/models/t5.js:21).
+  const float den = (float)log((double)max_distance / (double)max_exact);
+  const int n_rel = Lq + Lk - 1;
+  for (int idx = 0; idx < n_rel; ++idx) {
+    const int rel = idx - (Lq - 1);
+    int bucket = 0;
+    int n;
+    if (bidirectional) {
+      if (rel > 0) bucket = nb;
+      n = rel < 0 ? -rel : rel;
+    } else {
+      n = rel < 0 ? -rel : 0;
+    }
+    if (n < max_exact) {
+      bucket += n;
+    } else {
+      const float ratio = (float)n / (float)max_exact;
+      const float lg = (float)log((double)ratio);
+      const float scaled = (lg / den) * (float)(nb - max_exact);
+      int large = max_exact + (int)scaled;
+      if (large > nb - 1) large = nb - 1;
+      bucket += large;
+    }
+    out[idx] = bucket;
+  }
+  return ok();
+}
+
+int sa_t5_position_bias(const float* table, const int32_t* bucket_lut, int32_t num_buckets, int32_t H, int32_t Lq,
+                        int32_t Lk, float* out, void* stream) {
+  if (!table || !bucket_lut || !out) return fail(SA_ERR_INVALID, "table, bucket_lut and out must be non-NULL");
+  if (num_buckets < 1 || H < 1 || Lq < 1 || Lk < 1) return fail(SA_ERR_INVALID, "sizes must be >= 1");
+  hipError_t e = sa::launch_position_bias(table, bucket_lut, num_buckets, H, Lq, Lk, out, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "position_bias");
+  return ok();
+}
+
+int sa_device_count(int32_t* count) {
+  if (!count) return fail(SA_ERR_INVALID, "count is NULL");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) {
+    *count = 0;
+    return hip_fail(e, "hipGetDeviceCount");
+  }
+  *count = n;
+  return ok();
+}
+
+int sa_set_device(int32_t device) {
+  hipError_t e = hipSetDevice(device);
+  return e == hipSuccess ? ok() : hip_fail(e, "hipSetDevice");
+}
+
+int sa_malloc(void** ptr, size_t bytes) {
+  if (!ptr) return fail(SA_ERR_INVALID, "ptr is NULL");
+  *ptr = nullptr;
+  hipError_t e = hipMalloc(ptr, bytes == 0 ? 16 : bytes);
+  return e == hipSuccess ? ok() : hip_fail(e, "hipMalloc");
+}
+
+int sa_free(void* ptr) {
+  if (!ptr) return ok();
+  hipError_t e = hipFree(ptr);
+  return e == hipSuccess ? ok() : hip_fail(e, "hipFree");
+}
+
+int sa_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream) {
+  if (bytes == 0) return ok();
+  if (!dst || !src) return fail(SA_ERR_INVALID, "NULL pointer");
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)stream);
+  if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);  // the host buffer may be reused at once
+  return e == hipSuccess ? ok() : hip_fail(e, "memcpy h2d");
+}
+
+int sa_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream) {
+  if (bytes == 0) return ok();
+  if (!dst || !src) return fail(SA_ERR_INVALID, "NULL pointer");
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)stream);
+  if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "memcpy d2h");
+}
+
+int sa_memset(void* dst, int value, size_t bytes, void* stream) {
+  if (bytes == 0) return ok();
+  if (!dst) return fail(SA_ERR_INVALID, "NULL pointer");
+  hipError_t e = hipMemsetAsync(dst, value, bytes, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "hipMemsetAsync");
+}
+
+int sa_stream_create(void** stream) {
+  if (!stream) return fail(SA_ERR_INVALID, "stream is NULL");
+  hipStream_t s = nullptr;
+  hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+  *stream = s;
+  return e == hipSuccess ? ok() : hip_fail(e, "hipStreamCreateWithFlags");
+}
+
+int sa_stream_destroy(void* stream) {
+  if (!stream) return ok();
+  hipError_t e = hipStreamDestroy((hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "hipStreamDestroy");
+}
+
+int sa_stream_sync(void* stream) {
+  hipError_t e = hipStreamSynchronize((hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "hipStreamSynchronize");
+}
+
+int sa_device_sync(void) {
+  hipError_t e = hipDeviceSynchronize();
+  return e == hipSuccess ? ok() : hip_fail(e, "hipDeviceSynchronize");
+}
+
+int sa_event_create(void** event) {
+  if (!event) return fail(SA_ERR_INVALID, "event is NULL");
+  hipEvent_t ev = nullptr;
+  hipError_t e = hipEventCreate(&ev);
+  *event = ev;
+  return e == hipSuccess ? ok() : hip_fail(e, "hipEventCreate");
+}
+
+int sa_event_destroy(void* event) {
+  if (!event) return ok();
+  hipError_t e = hipEventDestroy((hipEvent_t)event);
+  return e == hipSuccess ? ok() : hip_fail(e, "hipEventDestroy");
+}
+
+int sa_event_record(void* event, void* stream) {
+  if (!event) return fail(SA_ERR_INVALID, "event is NULL");
+  hipError_t e = hipEventRecord((hipEvent_t)event, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "hipEventRecord");
+}
+
+int sa_event_elapsed_ms(float* ms, void* start, void* stop) {
+  if (!ms || !start || !stop) return fail(SA_ERR_INVALID, "NULL pointer");
+  hipError_t e = hipEventSynchronize((hipEvent_t)stop);
+  if (e == hipSuccess) e = hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop);
+  return e == hipSuccess ? ok() : hip_fail(e, "hipEventElapsedTime");
+}
+
+int sa_version(void) { return SA_ABI_VERSION; }
+
+const char* sa_last_error(void) { return g_err; }
+
+}  // extern "C"

@@ -1,0 +1,48 @@
+// Internal interface between the C ABI (api.hip) and the kernel translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sa {
+
+// Everything a kernel needs for one attention call, resolved and validated by the host.
+struct AttnParams {
+  const float* q;
+  const float* k;
+  const float* v;
+  float* o;
+  int64_t q_off, k_off, v_off, o_off;
+  int64_t ldq, ldk, ldv, ldo;
+  int64_t sq, sk, sv, so;
+  int B, H, D, Lq, Lk;
+  float scale_log2;  // softmax scale * log2(e): scores are kept in the base-2 domain
+  int bias_mode;
+  const float* bias;
+  int64_t sbias;
+  const int32_t* lut;
+  int num_buckets;
+  int mask_mode;
+  const int32_t* key_len;
+  const uint8_t* key_mask;
+  int64_t smask;
+};
+
+enum { BIAS_NONE = 0, BIAS_DENSE = 1, BIAS_RELPOS = 2 };
+enum { MASK_NONE = 0, MASK_KEY_LEN = 1, MASK_KEY_MASK = 2 };
+
+// Flash kernel on fp32 MFMA for D in {64, 128} with 16-byte aligned rows.
+// nsplit in {1, 2, 4}: key blocks are split across the 4 waves of a workgroup.
+hipError_t launch_flash_mfma(const AttnParams& p, int nsplit, hipStream_t stream);
+const char* flash_mfma_name(int D, int nsplit);
+
+// Any head dim up to 1024, any alignment: one workgroup per query row.
+hipError_t launch_generic(const AttnParams& p, hipStream_t stream);
+
+// Dense [H, Lq, Lk] relative-position bias from a table and bucket LUT.
+hipError_t launch_position_bias(const float* table, const int32_t* lut, int num_buckets, int H, int Lq,
+                                int Lk, float* out, hipStream_t stream);
+
+constexpr int GENERIC_MAX_D = 1024;
+
+}  // namespace sa

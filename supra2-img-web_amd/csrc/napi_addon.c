@@ -1,0 +1,485 @@
+/*
+ * Node.js N-API addon over the attention library's C ABI (include/supra_attn.h).
+ *
+ * It gives the JS shim (js/device.js, js/ops.js) what app/gpu/device.js gave app/gpu/ops.js:
+ * device buffers (GPU.empty / fromArray / read, device.js:144-191), one in-order queue
+ * (device.js:1-5: work is stream-ordered, so a buffer released right after a call is safe to
+ * reuse) and sync (device.js:255-259). The attention call itself maps ops.attention's options
+ * object (app/gpu/ops.js:109) onto sa_attn_args.
+ *
+ * Device pointers cross into JS as External values. Every C ABI status other than SA_OK becomes a
+ * thrown JS Error whose code is the status ("SA_ERR_INVALID", ...) and whose message is
+ * sa_last_error(). The stream is created on first use, so loading the addon on a host without a
+ * GPU succeeds (only calls that need the device fail).
+ */
+#include <node_api.h>
+
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "supra_attn.h"
+
+static void* g_stream = NULL;
+static int g_stream_ready = 0;
+
+#define NAPI_CALL(env, call)                                         \
+  do {                                                               \
+    napi_status st_ = (call);                                        \
+    if (st_ != napi_ok) {                                            \
+      const napi_extended_error_info* info_ = NULL;                  \
+      napi_get_last_error_info((env), &info_);                       \
+      napi_throw_error((env), "SA_NAPI",                             \
+                       info_ && info_->error_message                 \
+                           ? info_->error_message                    \
+                           : "N-API call failed");                   \
+      return NULL;                                                   \
+    }                                                                \
+  } while (0)
+
+static const char* status_code(int rc) {
+  switch (rc) {
+    case SA_ERR_INVALID: return "SA_ERR_INVALID";
+    case SA_ERR_UNSUPPORTED: return "SA_ERR_UNSUPPORTED";
+    case SA_ERR_HIP: return "SA_ERR_HIP";
+    case SA_ERR_ALIAS: return "SA_ERR_ALIAS";
+    default: return "SA_ERR";
+  }
+}
+
+/* Throws for a failed C ABI status; returns 1 if it threw. */
+static int throw_if(napi_env env, int rc) {
+  if (rc == SA_OK) return 0;
+  const char* msg = sa_last_error();
+  napi_throw_error(env, status_code(rc), msg && msg[0] ? msg : "supra_attn call failed");
+  return 1;
+}
+
+static int ensure_stream(napi_env env) {
+  if (g_stream_ready) return 0;
+  if (throw_if(env, sa_stream_create(&g_stream))) return 1;
+  g_stream_ready = 1;
+  return 0;
+}
+
+static napi_value undefined(napi_env env) {
+  napi_value u;
+  napi_get_undefined(env, &u);
+  return u;
+}
+
+static int get_args(napi_env env, napi_callback_info info, size_t want, napi_value* argv) {
+  size_t argc = want;
+  if (napi_get_cb_info(env, info, &argc, argv, NULL, NULL) != napi_ok) {
+    napi_throw_error(env, "SA_NAPI", "cannot read arguments");
+    return 1;
+  }
+  for (size_t i = argc; i < want; ++i) napi_get_undefined(env, &argv[i]);
+  return 0;
+}
+
+static int is_nullish(napi_env env, napi_value v) {
+  napi_valuetype t;
+  if (napi_typeof(env, v, &t) != napi_ok) return 1;
+  return t == napi_undefined || t == napi_null;
+}
+
+/* External -> pointer; undefined/null -> NULL. Anything else throws. */
+static int get_ptr(napi_env env, napi_value v, void** out, const char* what) {
+  *out = NULL;
+  if (is_nullish(env, v)) return 0;
+  napi_valuetype t;
+  napi_typeof(env, v, &t);
+  if (t != napi_external) {
+    char msg[128];
+    snprintf(msg, sizeof msg, "%s must be a device buffer handle", what);
+    napi_throw_type_error(env, "SA_ERR_INVALID", msg);
+    return 1;
+  }
+  return napi_get_value_external(env, v, out) == napi_ok ? 0 : 1;
+}
+
+static int get_i64(napi_env env, napi_value v, int64_t dflt, int64_t* out, const char* what) {
+  if (is_nullish(env, v)) {
+    *out = dflt;
+    return 0;
+  }
+  double d;
+  if (napi_get_value_double(env, v, &d) != napi_ok || d != d || d != (double)(int64_t)d) {
+    char msg[128];
+    snprintf(msg, sizeof msg, "%s must be an integer", what);
+    napi_throw_type_error(env, "SA_ERR_INVALID", msg);
+    return 1;
+  }
+  *out = (int64_t)d;
+  return 0;
+}
+
+static int get_f64(napi_env env, napi_value v, double dflt, double* out, const char* what) {
+  if (is_nullish(env, v)) {
+    *out = dflt;
+    return 0;
+  }
+  if (napi_get_value_double(env, v, out) != napi_ok) {
+    char msg[128];
+    snprintf(msg, sizeof msg, "%s must be a number", what);
+    napi_throw_type_error(env, "SA_ERR_INVALID", msg);
+    return 1;
+  }
+  return 0;
+}
+
+static int prop(napi_env env, napi_value obj, const char* name, napi_value* out) {
+  bool has = false;
+  if (napi_has_named_property(env, obj, name, &has) != napi_ok) return 1;
+  if (!has) {
+    napi_get_undefined(env, out);
+    return 0;
+  }
+  return napi_get_named_property(env, obj, name, out) == napi_ok ? 0 : 1;
+}
+
+static int prop_i64(napi_env env, napi_value obj, const char* name, int64_t dflt, int64_t* out) {
+  napi_value v;
+  if (prop(env, obj, name, &v)) return 1;
+  return get_i64(env, v, dflt, out, name);
+}
+
+static int prop_ptr(napi_env env, napi_value obj, const char* name, void** out) {
+  napi_value v;
+  if (prop(env, obj, name, &v)) return 1;
+  return get_ptr(env, v, out, name);
+}
+
+/* opts -> sa_attn_args. Field names are those of app/gpu/ops.js:109 (q, k, v, Lq, Lk, H, D, ldq,
+ * ldk, ldv, qOff, kOff, vOff, oOff, scale) plus out -> o, and the extension fields B, ldo, sq, sk,
+ * sv, so, biasMode, bias, sbias, bucketLut, numBuckets, maskMode, keyLen, keyMask, smask. */
+static int fill_args(napi_env env, napi_value o, sa_attn_args* a) {
+  memset(a, 0, sizeof *a);
+  a->struct_size = sizeof *a;
+  int64_t B, H, D, Lq, Lk, bm, mm, nb;
+  void *q, *k, *v, *out, *bias, *lut, *kl, *km;
+  double scale;
+  napi_value sv;
+  if (prop_i64(env, o, "B", 1, &B) || prop_i64(env, o, "H", -1, &H) || prop_i64(env, o, "D", -1, &D) ||
+      prop_i64(env, o, "Lq", -1, &Lq) || prop_i64(env, o, "Lk", -1, &Lk))
+    return 1;
+  if (prop_ptr(env, o, "q", &q) || prop_ptr(env, o, "k", &k) || prop_ptr(env, o, "v", &v) ||
+      prop_ptr(env, o, "out", &out) || prop_ptr(env, o, "bias", &bias) || prop_ptr(env, o, "bucketLut", &lut) ||
+      prop_ptr(env, o, "keyLen", &kl) || prop_ptr(env, o, "keyMask", &km))
+    return 1;
+  if (prop_i64(env, o, "qOff", 0, &a->q_off) || prop_i64(env, o, "kOff", 0, &a->k_off) ||
+      prop_i64(env, o, "vOff", 0, &a->v_off) || prop_i64(env, o, "oOff", 0, &a->o_off) ||
+      prop_i64(env, o, "ldq", -1, &a->ldq) || prop_i64(env, o, "ldk", -1, &a->ldk) ||
+      prop_i64(env, o, "ldv", -1, &a->ldv) || prop_i64(env, o, "ldo", 0, &a->ldo) ||
+      prop_i64(env, o, "sq", 0, &a->sq) || prop_i64(env, o, "sk", 0, &a->sk) || prop_i64(env, o, "sv", 0, &a->sv) ||
+      prop_i64(env, o, "so", 0, &a->so) || prop_i64(env, o, "sbias", 0, &a->sbias) ||
+      prop_i64(env, o, "smask", 0, &a->smask) || prop_i64(env, o, "biasMode", SA_BIAS_NONE, &bm) ||
+      prop_i64(env, o, "maskMode", SA_MASK_NONE, &mm) || prop_i64(env, o, "numBuckets", 0, &nb))
+    return 1;
+  if (prop(env, o, "scale", &sv) || get_f64(env, sv, 1.0, &scale, "scale")) return 1;
+  if (B < -0x7fffffffLL || B > 0x7fffffffLL || H > 0x7fffffffLL || D > 0x7fffffffLL || Lq > 0x7fffffffLL ||
+      Lk > 0x7fffffffLL) {
+    napi_throw_range_error(env, "SA_ERR_INVALID", "sizes must fit in int32");
+    return 1;
+  }
+  a->B = (int32_t)B;
+  a->H = (int32_t)H;
+  a->D = (int32_t)D;
+  a->Lq = (int32_t)Lq;
+  a->Lk = (int32_t)Lk;
+  a->q = (const float*)q;
+  a->k = (const float*)k;
+  a->v = (const float*)v;
+  a->o = (float*)out;
+  a->scale = (float)scale;
+  a->bias_mode = (int32_t)bm;
+  a->bias = (const float*)bias;
+  a->bucket_lut = (const int32_t*)lut;
+  a->num_buckets = (int32_t)nb;
+  a->mask_mode = (int32_t)mm;
+  a->key_len = (const int32_t*)kl;
+  a->key_mask = (const uint8_t*)km;
+  return 0;
+}
+
+static napi_value js_attention(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (get_args(env, info, 1, argv)) return NULL;
+  sa_attn_args a;
+  if (fill_args(env, argv[0], &a)) return NULL;
+  /* validate before touching the device, so a bad call reports its own error on any host */
+  if (sa_attention_kernel_name(&a) == NULL) {
+    throw_if(env, SA_ERR_INVALID);
+    return NULL;
+  }
+  if (ensure_stream(env)) return NULL;
+  if (throw_if(env, sa_attention_f32(&a, g_stream))) return NULL;
+  return undefined(env);
+}
+
+static napi_value js_kernel_name(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (get_args(env, info, 1, argv)) return NULL;
+  sa_attn_args a;
+  if (fill_args(env, argv[0], &a)) return NULL;
+  const char* name = sa_attention_kernel_name(&a);
+  if (!name) {
+    throw_if(env, SA_ERR_INVALID);
+    return NULL;
+  }
+  napi_value r;
+  NAPI_CALL(env, napi_create_string_utf8(env, name, NAPI_AUTO_LENGTH, &r));
+  return r;
+}
+
+static napi_value js_version(napi_env env, napi_callback_info info) {
+  (void)info;
+  napi_value r;
+  NAPI_CALL(env, napi_create_int32(env, sa_version(), &r));
+  return r;
+}
+
+static napi_value js_device_count(napi_env env, napi_callback_info info) {
+  (void)info;
+  int32_t n = 0;
+  sa_device_count(&n); /* 0 when no device is visible */
+  napi_value r;
+  NAPI_CALL(env, napi_create_int32(env, n, &r));
+  return r;
+}
+
+static napi_value js_malloc(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (get_args(env, info, 1, argv)) return NULL;
+  int64_t bytes;
+  if (get_i64(env, argv[0], -1, &bytes, "bytes")) return NULL;
+  if (bytes < 0) {
+    napi_throw_range_error(env, "SA_ERR_INVALID", "bytes must be >= 0");
+    return NULL;
+  }
+  void* p = NULL;
+  if (throw_if(env, sa_malloc(&p, (size_t)bytes))) return NULL;
+  napi_value r;
+  NAPI_CALL(env, napi_create_external(env, p, NULL, NULL, &r));
+  return r;
+}
+
+static napi_value js_free(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (get_args(env, info, 1, argv)) return NULL;
+  void* p;
+  if (get_ptr(env, argv[0], &p, "buffer")) return NULL;
+  if (g_stream_ready && throw_if(env, sa_stream_sync(g_stream))) return NULL;
+  if (throw_if(env, sa_free(p))) return NULL;
+  return undefined(env);
+}
+
+/* (buffer, typedArray, byteOffset) -> the typed array's bytes at buffer + byteOffset */
+static int typed_bytes(napi_env env, napi_value ta, void** data, size_t* bytes) {
+  bool is_ta = false;
+  napi_is_typedarray(env, ta, &is_ta);
+  if (!is_ta) {
+    napi_throw_type_error(env, "SA_ERR_INVALID", "expected a TypedArray");
+    return 1;
+  }
+  napi_typedarray_type type;
+  size_t length, offset;
+  napi_value ab;
+  if (napi_get_typedarray_info(env, ta, &type, &length, data, &ab, &offset) != napi_ok) {
+    napi_throw_error(env, "SA_NAPI", "cannot read TypedArray");
+    return 1;
+  }
+  size_t elem = 1;
+  switch (type) {
+    case napi_int16_array: case napi_uint16_array: elem = 2; break;
+    case napi_int32_array: case napi_uint32_array: case napi_float32_array: elem = 4; break;
+    case napi_float64_array: case napi_bigint64_array: case napi_biguint64_array: elem = 8; break;
+    default: elem = 1; break;
+  }
+  *bytes = length * elem;
+  return 0;
+}
+
+static napi_value js_upload(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (get_args(env, info, 3, argv)) return NULL;
+  void* dst;
+  void* src;
+  size_t bytes;
+  int64_t off;
+  if (get_ptr(env, argv[0], &dst, "buffer") || typed_bytes(env, argv[1], &src, &bytes) ||
+      get_i64(env, argv[2], 0, &off, "byteOffset"))
+    return NULL;
+  if (!dst || off < 0) {
+    napi_throw_error(env, "SA_ERR_INVALID", "upload needs a buffer and byteOffset >= 0");
+    return NULL;
+  }
+  if (ensure_stream(env)) return NULL;
+  if (throw_if(env, sa_memcpy_h2d((char*)dst + off, src, bytes, g_stream))) return NULL;
+  return undefined(env);
+}
+
+static napi_value js_download(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (get_args(env, info, 3, argv)) return NULL;
+  void* src;
+  void* dst;
+  size_t bytes;
+  int64_t off;
+  if (get_ptr(env, argv[0], &src, "buffer") || typed_bytes(env, argv[1], &dst, &bytes) ||
+      get_i64(env, argv[2], 0, &off, "byteOffset"))
+    return NULL;
+  if (!src || off < 0) {
+    napi_throw_error(env, "SA_ERR_INVALID", "download needs a buffer and byteOffset >= 0");
+    return NULL;
+  }
+  if (ensure_stream(env)) return NULL;
+  if (throw_if(env, sa_memcpy_d2h(dst, (const char*)src + off, bytes, g_stream))) return NULL;
+  return argv[1];
+}
+
+static napi_value js_memset(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (get_args(env, info, 3, argv)) return NULL;
+  void* dst;
+  int64_t value, bytes;
+  if (get_ptr(env, argv[0], &dst, "buffer") || get_i64(env, argv[1], 0, &value, "value") ||
+      get_i64(env, argv[2], -1, &bytes, "bytes"))
+    return NULL;
+  if (bytes < 0) {
+    napi_throw_range_error(env, "SA_ERR_INVALID", "bytes must be >= 0");
+    return NULL;
+  }
+  if (ensure_stream(env)) return NULL;
+  if (throw_if(env, sa_memset(dst, (int)value, (size_t)bytes, g_stream))) return NULL;
+  return undefined(env);
+}
+
+static napi_value js_sync(napi_env env, napi_callback_info info) {
+  (void)info;
+  if (ensure_stream(env)) return NULL;
+  if (throw_if(env, sa_stream_sync(g_stream))) return NULL;
+  return undefined(env);
+}
+
+static napi_value js_bucket_lut(napi_env env, napi_callback_info info) {
+  napi_value argv[5];
+  if (get_args(env, info, 5, argv)) return NULL;
+  int64_t Lq, Lk, nb, md, bidir;
+  if (get_i64(env, argv[0], -1, &Lq, "Lq") || get_i64(env, argv[1], -1, &Lk, "Lk") ||
+      get_i64(env, argv[2], 32, &nb, "numBuckets") || get_i64(env, argv[3], 128, &md, "maxDistance"))
+    return NULL;
+  bool b = true;
+  if (!is_nullish(env, argv[4]) && napi_get_value_bool(env, argv[4], &b) != napi_ok) {
+    napi_throw_type_error(env, "SA_ERR_INVALID", "bidirectional must be a boolean");
+    return NULL;
+  }
+  bidir = b ? 1 : 0;
+  if (Lq < 1 || Lk < 1 || Lq > 0x3fffffff || Lk > 0x3fffffff) {
+    napi_throw_range_error(env, "SA_ERR_INVALID", "Lq and Lk must be in [1, 2^30)");
+    return NULL;
+  }
+  const size_t n = (size_t)(Lq + Lk - 1);
+  napi_value ab, arr;
+  void* data = NULL;
+  NAPI_CALL(env, napi_create_arraybuffer(env, n * sizeof(int32_t), &data, &ab));
+  if (throw_if(env, sa_t5_bucket_lut((int32_t)Lq, (int32_t)Lk, (int32_t)nb, (int32_t)md, (int32_t)bidir,
+                                     (int32_t*)data)))
+    return NULL;
+  NAPI_CALL(env, napi_create_typedarray(env, napi_int32_array, n, ab, 0, &arr));
+  return arr;
+}
+
+static napi_value js_position_bias(napi_env env, napi_callback_info info) {
+  napi_value argv[7];
+  if (get_args(env, info, 7, argv)) return NULL;
+  void *table, *lut, *out;
+  int64_t nb, H, Lq, Lk;
+  if (get_ptr(env, argv[0], &table, "table") || get_ptr(env, argv[1], &lut, "bucketLut") ||
+      get_i64(env, argv[2], -1, &nb, "numBuckets") || get_i64(env, argv[3], -1, &H, "H") ||
+      get_i64(env, argv[4], -1, &Lq, "Lq") || get_i64(env, argv[5], -1, &Lk, "Lk") ||
+      get_ptr(env, argv[6], &out, "out"))
+    return NULL;
+  if (ensure_stream(env)) return NULL;
+  if (throw_if(env, sa_t5_position_bias((const float*)table, (const int32_t*)lut, (int32_t)nb, (int32_t)H,
+                                        (int32_t)Lq, (int32_t)Lk, (float*)out, g_stream)))
+    return NULL;
+  return undefined(env);
+}
+
+static napi_value js_event_create(napi_env env, napi_callback_info info) {
+  (void)info;
+  void* ev = NULL;
+  if (throw_if(env, sa_event_create(&ev))) return NULL;
+  napi_value r;
+  NAPI_CALL(env, napi_create_external(env, ev, NULL, NULL, &r));
+  return r;
+}
+
+static napi_value js_event_record(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (get_args(env, info, 1, argv)) return NULL;
+  void* ev;
+  if (get_ptr(env, argv[0], &ev, "event")) return NULL;
+  if (ensure_stream(env)) return NULL;
+  if (throw_if(env, sa_event_record(ev, g_stream))) return NULL;
+  return undefined(env);
+}
+
+static napi_value js_event_elapsed(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (get_args(env, info, 2, argv)) return NULL;
+  void *a, *b;
+  if (get_ptr(env, argv[0], &a, "start") || get_ptr(env, argv[1], &b, "stop")) return NULL;
+  float ms = 0.f;
+  if (throw_if(env, sa_event_elapsed_ms(&ms, a, b))) return NULL;
+  napi_value r;
+  NAPI_CALL(env, napi_create_double(env, ms, &r));
+  return r;
+}
+
+static napi_value js_event_destroy(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (get_args(env, info, 1, argv)) return NULL;
+  void* ev;
+  if (get_ptr(env, argv[0], &ev, "event")) return NULL;
+  if (throw_if(env, sa_event_destroy(ev))) return NULL;
+  return undefined(env);
+}
+
+static napi_value init(napi_env env, napi_value exports) {
+  const napi_property_descriptor props[] = {
+      {"attention", NULL, js_attention, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"kernelName", NULL, js_kernel_name, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"version", NULL, js_version, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"deviceCount", NULL, js_device_count, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"malloc", NULL, js_malloc, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"free", NULL, js_free, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"upload", NULL, js_upload, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"download", NULL, js_download, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"memset", NULL, js_memset, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"sync", NULL, js_sync, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"bucketLut", NULL, js_bucket_lut, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"positionBias", NULL, js_position_bias, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"eventCreate", NULL, js_event_create, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"eventRecord", NULL, js_event_record, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"eventElapsed", NULL, js_event_elapsed, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"eventDestroy", NULL, js_event_destroy, NULL, NULL, NULL, napi_enumerable, NULL},
+  };
+  NAPI_CALL(env, napi_define_properties(env, exports, sizeof props / sizeof props[0], props));
+  napi_value c;
+#define CONST(name, val)                                      \
+  NAPI_CALL(env, napi_create_int32(env, (val), &c));          \
+  NAPI_CALL(env, napi_set_named_property(env, exports, name, c));
+  CONST("SA_BIAS_NONE", SA_BIAS_NONE)
+  CONST("SA_BIAS_DENSE", SA_BIAS_DENSE)
+  CONST("SA_BIAS_RELPOS", SA_BIAS_RELPOS)
+  CONST("SA_MASK_NONE", SA_MASK_NONE)
+  CONST("SA_MASK_KEY_LEN", SA_MASK_KEY_LEN)
+  CONST("SA_MASK_KEY_MASK", SA_MASK_KEY_MASK)
+#undef CONST
+  return exports;
+}
+
+NAPI_MODULE(NODE_GYP_MODULE_NAME, init)

@@ -1,0 +1,159 @@
+"""ctypes binding of libsupra_attn.so (include/supra_attn.h).
+
+Loading fails loudly when the library has not been built: there is no other implementation of the
+operator behind this module.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t, c_uint32, c_void_p
+
+PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG, "lib", "libsupra_attn.so")
+
+SA_OK = 0
+SA_ERR_INVALID = -1
+SA_ERR_UNSUPPORTED = -2
+SA_ERR_HIP = -3
+SA_ERR_ALIAS = -4
+
+SA_BIAS_NONE = 0
+SA_BIAS_DENSE = 1
+SA_BIAS_RELPOS = 2
+
+SA_MASK_NONE = 0
+SA_MASK_KEY_LEN = 1
+SA_MASK_KEY_MASK = 2
+
+# Every symbol include/supra_attn.h declares, with (restype, argtypes).
+SIGNATURES = {
+    "sa_attention_f32": (c_int, [c_void_p, c_void_p]),
+    "sa_attention_kernel_name": (c_char_p, [c_void_p]),
+    "sa_t5_bucket_lut": (c_int, [c_int32, c_int32, c_int32, c_int32, c_int32, POINTER(c_int32)]),
+    "sa_t5_position_bias": (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p]),
+    "sa_device_count": (c_int, [POINTER(c_int32)]),
+    "sa_set_device": (c_int, [c_int32]),
+    "sa_malloc": (c_int, [POINTER(c_void_p), c_size_t]),
+    "sa_free": (c_int, [c_void_p]),
+    "sa_memcpy_h2d": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
+    "sa_memcpy_d2h": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
+    "sa_memset": (c_int, [c_void_p, c_int, c_size_t, c_void_p]),
+    "sa_stream_create": (c_int, [POINTER(c_void_p)]),
+    "sa_stream_destroy": (c_int, [c_void_p]),
+    "sa_stream_sync": (c_int, [c_void_p]),
+    "sa_device_sync": (c_int, []),
+    "sa_event_create": (c_int, [POINTER(c_void_p)]),
+    "sa_event_destroy": (c_int, [c_void_p]),
+    "sa_event_record": (c_int, [c_void_p, c_void_p]),
+    "sa_event_elapsed_ms": (c_int, [POINTER(c_float), c_void_p, c_void_p]),
+    "sa_version": (c_int, []),
+    "sa_last_error": (c_char_p, []),
+}
+
+
+class SaError(RuntimeError):
+    """A non-zero status from the C ABI, with its code and sa_last_error() message."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"supra_attn error {code}: {message}")
+        self.code = code
+        self.message = message
+
+
+class AttnArgs(ctypes.Structure):
+    """Mirror of sa_attn_args (include/supra_attn.h)."""
+
+    _fields_ = [
+        ("struct_size", c_uint32),
+        ("B", c_int32),
+        ("H", c_int32),
+        ("D", c_int32),
+        ("Lq", c_int32),
+        ("Lk", c_int32),
+        ("q", c_void_p),
+        ("k", c_void_p),
+        ("v", c_void_p),
+        ("o", c_void_p),
+        ("q_off", c_int64),
+        ("k_off", c_int64),
+        ("v_off", c_int64),
+        ("o_off", c_int64),
+        ("ldq", c_int64),
+        ("ldk", c_int64),
+        ("ldv", c_int64),
+        ("ldo", c_int64),
+        ("sq", c_int64),
+        ("sk", c_int64),
+        ("sv", c_int64),
+        ("so", c_int64),
+        ("scale", c_float),
+        ("bias_mode", c_int32),
+        ("bias", c_void_p),
+        ("sbias", c_int64),
+        ("bucket_lut", c_void_p),
+        ("num_buckets", c_int32),
+        ("mask_mode", c_int32),
+        ("key_len", c_void_p),
+        ("key_mask", c_void_p),
+        ("smask", c_int64),
+    ]
+
+    def __init__(self, **kw):
+        super().__init__()
+        self.struct_size = ctypes.sizeof(AttnArgs)
+        for name, val in kw.items():
+            setattr(self, name, val)
+
+
+_LIB = None
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load the library once (raises if it has not been built)."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: build it with `python supra2-img-web_amd/build.py`")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _LIB = lib
+    return lib
+
+
+def check(rc: int) -> None:
+    if rc != SA_OK:
+        msg = load().sa_last_error()
+        raise SaError(rc, msg.decode() if msg else "")
+
+
+def attention(args: AttnArgs, stream: int | None = None) -> None:
+    check(load().sa_attention_f32(ctypes.byref(args), stream))
+
+
+def kernel_name(args: AttnArgs) -> str:
+    lib = load()
+    name = lib.sa_attention_kernel_name(ctypes.byref(args))
+    if name is None:
+        raise SaError(-1, lib.sa_last_error().decode())
+    return name.decode()
+
+
+def bucket_lut(Lq: int, Lk: int, num_buckets: int = 32, max_distance: int = 128, bidirectional: bool = True):
+    import numpy as np
+
+    out = np.zeros(Lq + Lk - 1, dtype=np.int32)
+    check(load().sa_t5_bucket_lut(Lq, Lk, num_buckets, max_distance, int(bidirectional),
+                                  out.ctypes.data_as(POINTER(c_int32))))
+    return out
+
+
+def device_count() -> int:
+    n = c_int32(0)
+    rc = load().sa_device_count(ctypes.byref(n))
+    return n.value if rc == SA_OK else 0

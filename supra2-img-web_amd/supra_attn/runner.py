@@ -1,0 +1,63 @@
+"""Stage a workload `Call` on the device and run it through sa_attention_f32."""
+
+from __future__ import annotations
+
+import numpy as np
+
+from . import _lib
+from .device import Device
+from .workloads import Call
+
+
+class Staged:
+    """Device-resident buffers of one call plus its ready-to-launch sa_attn_args."""
+
+    def __init__(self, dev: Device, call: Call, out_fill: float | None = None):
+        self.dev = dev
+        self.call = call
+        self.bufs = []
+        q = self._put(call.q)
+        k = q if call.same_qkv else self._put(call.k)
+        v = q if call.same_qkv else (k if call.v is call.k else self._put(call.v))
+        self.out = dev.empty(call.out_shape)
+        self.bufs.append(self.out)
+        if out_fill is not None:
+            self.out.upload(np.full(call.out_shape, out_fill, dtype=np.float32))
+        a = dict(call.args)
+        kw = dict(B=call.B, H=call.H, D=call.D, Lq=call.Lq, Lk=call.Lk, q=q.ptr, k=k.ptr, v=v.ptr,
+                  o=self.out.ptr, scale=call.scale, bias_mode=call.bias_mode, mask_mode=call.mask_mode)
+        kw.update(a)
+        if call.bias is not None:
+            kw["bias"] = self._put(call.bias).ptr
+        if call.lut is not None:
+            kw["bucket_lut"] = self._put(np.asarray(call.lut, dtype=np.int32)).ptr
+            kw["num_buckets"] = int(call.bias.shape[0])
+        if call.key_len is not None:
+            kw["key_len"] = self._put(np.asarray(call.key_len, dtype=np.int32)).ptr
+        if call.key_mask is not None:
+            km = np.asarray(call.key_mask, dtype=np.uint8)
+            kw["key_mask"] = self._put(km).ptr
+            kw.setdefault("smask", km.shape[-1])
+        self.args = _lib.AttnArgs(**kw)
+
+    def _put(self, arr):
+        buf = self.dev.from_array(np.ascontiguousarray(arr))
+        self.bufs.append(buf)
+        return buf
+
+    def launch(self) -> None:
+        self.dev.attention(self.args)
+
+    def run(self) -> np.ndarray:
+        self.launch()
+        self.dev.sync()
+        return self.out.read()
+
+    @property
+    def kernel(self) -> str:
+        return _lib.kernel_name(self.args)
+
+    def release(self) -> None:
+        for b in self.bufs:
+            b.release()
+        self.bufs = []

@@ -1,0 +1,178 @@
+"""GPU parity: the HIP operator, called through the C ABI, against the CPU oracle.
+
+The bar (the PyTorch fp32 CPU path, oracle.attention.attention_torch_fp32): relative L2 and
+normwise max relative error both <= 1e-5; the fp64 brute force is checked with the same bound.
+Output elements outside the written rows must keep their previous contents.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import attention as orc
+from supra_attn import _lib, workloads
+from supra_attn.runner import Staged
+from cases import make_call
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+SENTINEL = np.float32(-12345.5)
+
+
+def run_checked(dev, call, *, expect_kernel=None, tol=TOL, check_fp64=True):
+    print(f"[case] {call.name} B={call.B} H={call.H} D={call.D} Lq={call.Lq} Lk={call.Lk} "
+          f"bias={call.bias_mode} mask={call.mask_mode}", flush=True)
+    st = Staged(dev, call, out_fill=SENTINEL)
+    try:
+        if expect_kernel is not None:
+            assert st.kernel == expect_kernel
+        out = st.run()
+    finally:
+        st.release()
+    got = orc.output_view(out, call)
+    ref = orc.reference_torch(call)
+    e = orc.errors(got, ref)
+    assert e["finite"], f"non-finite output for {call.name}"
+    assert e["rel_l2"] <= tol and e["max_rel"] <= tol, f"{call.name} vs torch fp32: {e}"
+    if check_fp64:
+        e64 = orc.errors(got, orc.reference_fp64(call))
+        assert e64["rel_l2"] <= tol and e64["max_rel"] <= tol, f"{call.name} vs fp64: {e64}"
+    # untouched elements of the output buffer keep the sentinel
+    written = np.zeros(out.size, dtype=bool)
+    a = call.args
+    ldo = a.get("ldo", 0) or call.H * call.D
+    idx = orc.heads(np.arange(out.size), B=call.B, L=call.Lq, H=call.H, D=call.D, off=a.get("o_off", 0), ld=ldo,
+                    sb=a.get("so", 0))
+    written[idx.reshape(-1)] = True
+    assert (out.reshape(-1)[~written] == SENTINEL).all(), "operator wrote outside its output rows"
+    return e
+
+
+# ---- the four single-call configs
+
+
+def test_dit_self_b2(dev):
+    call = workloads.dit_self(B=2, seed=0)
+    run_checked(dev, call, expect_kernel="flash_mfma_d64_split4")
+
+
+def test_dit_cross_b2(dev):
+    call = workloads.dit_cross(B=2, seed=1)
+    run_checked(dev, call)
+
+
+def test_t5_relpos_keymask(dev):
+    call = workloads.t5_self(seed=2)
+    run_checked(dev, call)
+
+
+def test_vae_mid(dev):
+    call = workloads.vae_mid(seed=3)
+    run_checked(dev, call)
+
+
+def test_sweep_block0(dev):
+    s, c = workloads.sweep_block(0)
+    run_checked(dev, s, expect_kernel="flash_mfma_d64", check_fp64=False)
+    run_checked(dev, c, expect_kernel="flash_mfma_d64", check_fp64=False)
+
+
+# ---- shapes, layouts and splits
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("Lq,Lk", [(1, 1), (32, 32), (77, 45), (130, 257), (256, 31)])
+def test_shapes(dev, D, Lq, Lk):
+    run_checked(dev, make_call(B=2, H=3, D=D, Lq=Lq, Lk=Lk, seed=Lq * 1000 + Lk))
+
+
+@pytest.mark.parametrize("B,H,Lq,Lk", [(1, 1, 64, 256), (4, 9, 256, 256), (64, 9, 256, 256), (8, 16, 512, 96)])
+def test_split_modes(dev, B, H, Lq, Lk):
+    """Work sizes that select each key-split variant of the MFMA kernel."""
+    run_checked(dev, make_call(B=B, H=H, D=64, Lq=Lq, Lk=Lk, seed=B * H + Lk, packed=True), check_fp64=(B < 64))
+
+
+def test_packed_offsets_padded_rows(dev):
+    call = make_call(B=3, H=4, D=64, Lq=100, Lk=70, packed=True, pad_cols=8, q_off=12, o_off=20, ldo_pad=36, seed=7)
+    run_checked(dev, call)
+
+
+def test_scale_values(dev):
+    for sc in (1.0, 0.01, 3.0, -0.5):
+        run_checked(dev, make_call(B=1, H=2, D=64, Lq=40, Lk=90, scale=sc, seed=11))
+
+
+# ---- masks and bias
+
+
+def test_key_len_including_zero(dev):
+    call = make_call(B=6, H=2, D=64, Lq=64, Lk=128, mask_mode=_lib.SA_MASK_KEY_LEN,
+                     key_len=[0, 1, 31, 32, 33, 128], seed=3)
+    run_checked(dev, call)
+
+
+def test_key_mask_random_and_empty(dev):
+    call = make_call(B=3, H=2, D=64, Lq=50, Lk=100, mask_mode=_lib.SA_MASK_KEY_MASK, seed=5)
+    call.key_mask[1, :] = 0  # a sequence with no attended key -> zeros
+    run_checked(dev, call)
+
+
+@pytest.mark.parametrize("batched", [False, True])
+def test_dense_bias(dev, batched):
+    call = make_call(B=2, H=3, D=64, Lq=70, Lk=90, bias_mode=_lib.SA_BIAS_DENSE, dense_bias_batched=batched, seed=9)
+    run_checked(dev, call)
+
+
+@pytest.mark.parametrize("Lq,Lk", [(128, 128), (37, 200), (300, 20)])
+def test_relpos_bias(dev, Lq, Lk):
+    call = make_call(B=2, H=12, D=64, Lq=Lq, Lk=Lk, scale=1.0, bias_mode=_lib.SA_BIAS_RELPOS,
+                     mask_mode=_lib.SA_MASK_KEY_LEN, key_len=[Lk, max(1, Lk - 40)], seed=Lq + Lk)
+    run_checked(dev, call)
+
+
+def test_relpos_matches_dense(dev):
+    """The in-kernel relative-position gather equals passing its dense expansion."""
+    c1 = make_call(B=1, H=12, D=64, Lq=128, Lk=128, scale=1.0, bias_mode=_lib.SA_BIAS_RELPOS, seed=21)
+    c2 = make_call(B=1, H=12, D=64, Lq=128, Lk=128, scale=1.0, seed=21)
+    c2.bias = orc.dense_relpos_bias(c1.bias, c1.lut, 12, 128, 128)[None]
+    c2.bias_mode = _lib.SA_BIAS_DENSE
+    o1 = Staged(dev, c1).run()
+    o2 = Staged(dev, c2).run()
+    assert orc.errors(o1, o2)["max_rel"] <= 1e-6
+
+
+# ---- generic kernel (head dims / alignment outside the MFMA kernels)
+
+
+@pytest.mark.parametrize("D", [1, 32, 80, 512])
+def test_generic_head_dims(dev, D):
+    call = make_call(B=2, H=2, D=D, Lq=33, Lk=300, seed=D)
+    name = _lib.kernel_name(Staged(dev, call).args)
+    assert name == "generic"
+    run_checked(dev, call)
+
+
+def test_generic_unaligned(dev):
+    call = make_call(B=2, H=3, D=64, Lq=40, Lk=50, pad_cols=1, seed=4, bias_mode=_lib.SA_BIAS_RELPOS,
+                     mask_mode=_lib.SA_MASK_KEY_MASK)
+    st = Staged(dev, call)
+    assert st.kernel == "generic"
+    run_checked(dev, call)
+
+
+def test_position_bias_builder(dev):
+    """sa_t5_position_bias writes the dense [H, Lq, Lk] bias of app/models/t5.js:55-65."""
+    import ctypes
+
+    rng = np.random.default_rng(0)
+    H, Lq, Lk = 12, 50, 70
+    table = rng.standard_normal((32, H), dtype=np.float32)
+    lut = _lib.bucket_lut(Lq, Lk)
+    tb = dev.from_array(table)
+    lb = dev.from_array(lut)
+    out = dev.empty((H, Lq, Lk))
+    _lib.check(_lib.load().sa_t5_position_bias(tb.ptr, lb.ptr, 32, H, Lq, Lk, out.ptr, ctypes.c_void_p(dev.stream)))
+    dev.sync()
+    np.testing.assert_array_equal(out.read(), orc.dense_relpos_bias(table, lut, H, Lq, Lk))
