@@ -13,6 +13,11 @@ The same JSON line carries:
   cpu_baseline the PyTorch fp32 CPU formulation of tools/reference.py:72-79 on a bounded sample
 
     python bench.py [--steps 50] [--warmup 3] [--cpu-steps 4] [--no-cpu]
+
+`--profile WORKLOAD` instead launches one workload (sweep_self, sweep_cross or a single-call
+config) `--launches` times, then copies a 256 MiB device buffer 4 times with the runtime's copy
+kernel: a short program for rocprofv3 counter passes, whose per-dispatch FETCH_SIZE/WRITE_SIZE of
+the copy (known bytes) calibrate the attention kernel's HBM traffic.
 """
 
 from __future__ import annotations
@@ -98,6 +103,37 @@ def cpu_baseline(data, steps: int) -> dict:
     }
 
 
+COPY_BYTES = 256 << 20
+
+
+def profile_run(workload: str, launches: int) -> int:
+    import ctypes
+
+    from supra_attn import _lib, workloads
+    from supra_attn.device import Device
+    from supra_attn.runner import Staged
+
+    dev = Device(0)
+    if workload in ("sweep_self", "sweep_cross"):
+        s, c = workloads.SweepData(blocks=1).block(0)
+        call = s if workload == "sweep_self" else c
+    else:
+        call = workloads.CONFIGS[workload]()
+    st = Staged(dev, call)
+    log(f"profile {workload}: {launches} launches of {st.kernel}, "
+        f"{call.flops()} flop and {call.algorithmic_bytes()} algorithmic bytes per launch")
+    for _ in range(launches):
+        st.launch()
+    dev.sync()
+    src, dst = dev.empty((COPY_BYTES // 4,)), dev.empty((COPY_BYTES // 4,))
+    src.fill_bytes(0)
+    for _ in range(4):
+        _lib.check(_lib.load().sa_memcpy_d2d(dst.ptr, src.ptr, COPY_BYTES, ctypes.c_void_p(dev.stream)))
+    dev.sync()
+    log(f"profile {workload}: done ({COPY_BYTES} bytes per calibration copy)")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -106,12 +142,16 @@ def main() -> int:
     ap.add_argument("--cpu-steps", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calls", type=int, default=200, help="calls per single-config timing")
+    ap.add_argument("--profile", default=None, help="launch only this workload (for rocprofv3 counter passes)")
+    ap.add_argument("--launches", type=int, default=20)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this operator's path has no multi-GPU form here (asked for --gpus {args.gpus}); "
               "the per-GPU shard of a sharded run is the same kernel at the shapes measured with --gpus 1.",
               file=sys.stderr)
         return 2
+    if args.profile:
+        return profile_run(args.profile, args.launches)
 
     from supra_attn import workloads
     from supra_attn.device import Device, Event

@@ -124,8 +124,9 @@ int sa_device_count(int32_t* count);
 int sa_set_device(int32_t device);
 int sa_malloc(void** ptr, size_t bytes);   /* device memory; synchronous */
 int sa_free(void* ptr);                    /* synchronous (waits for the device) */
-int sa_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream); /* stream-ordered */
+int sa_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream); /* returns when copied */
 int sa_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream); /* waits for stream */
+int sa_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream); /* stream-ordered */
 int sa_memset(void* dst, int value, size_t bytes, void* stream);
 int sa_stream_create(void** stream);       /* a non-blocking stream at the default priority */
 int sa_stream_destroy(void* stream);

@@ -27,6 +27,8 @@ HIP_SOURCES = ["api.hip", "flash_mfma.hip", "generic.hip"]
 ARCH = "gfx950"
 # Packed FP32 instructions are kept out of the device code (they are emitted from plain float
 # code at -O3 otherwise); the host pass warns that it does not know the feature.
+# MFMA accumulators are kept in ordinary VGPRs: with the AGPR form the compiler copies the
+# score and output tiles between register files around every softmax step.
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -34,6 +36,7 @@ HIP_FLAGS = [
     "-fPIC",
     "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 NODE_INCLUDE = "/usr/include/node"
 

@@ -304,6 +304,13 @@ int sa_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream) {
   return e == hipSuccess ? ok() : hip_fail(e, "memcpy d2h");
 }
 
+int sa_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
+  if (bytes == 0) return ok();
+  if (!dst || !src) return fail(SA_ERR_INVALID, "NULL pointer");
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "memcpy d2d");
+}
+
 int sa_memset(void* dst, int value, size_t bytes, void* stream) {
   if (bytes == 0) return ok();
   if (!dst) return fail(SA_ERR_INVALID, "NULL pointer");

@@ -24,12 +24,21 @@
 //   O^T accumulates in D/32 tiles of 16 registers: lane l holds query l%32, dims
 //   32*t + 8*(r/4) + 4*(l/32) + r%4.
 //
-// Softmax arithmetic (base 2): u = s*scale*log2(e) + bias*log2(e); masked keys get u = -inf;
-//   m = running max (seeded with -FLT_MAX), p = exp2(u - m), alpha = exp2(m_old - m_new),
-//   l = l*alpha + sum p, O = O*alpha + P V; output O / l, or 0 when every key is masked.
+// Softmax arithmetic (base 2): Q is pre-multiplied by scale*log2(e) when it is loaded, so the MFMA
+//   produces u = s*scale*log2(e) directly; u += bias*log2(e); masked keys get u = -inf.
+//   m = running reference (seeded with -FLT_MAX), p = exp2(u - m), l = sum p, O = sum p V;
+//   output O / l, or 0 when every key is masked. The reference is moved (O and l rescaled by
+//   alpha = exp2(m_old - m_new)) only when some row's block maximum exceeds it by more than
+//   kRescaleSlack: otherwise p <= 2^kRescaleSlack and numerator and denominator share the same
+//   stale reference, so the quotient is unchanged while most blocks skip the rescale.
 //
-// LDS: K tile [KT keys][D+4] (b128 reads of 16 consecutive rows hit distinct banks),
-//      V tile [KT keys][D+8] (rows 4 apart land 32 banks apart for the two half-waves).
+// K/V tiles move HBM -> LDS with global_load_lds_dwordx4 (no VGPR staging), double-buffered: the
+// next tile streams in while the current one is consumed, one barrier per key block. Rows past the
+// last valid key re-read the last valid row (finite data, masked out of the softmax).
+// LDS tiles are [KT keys][D] in 16-byte chunks, XOR-swizzled per row:
+//   K: chunk c of row r at c ^ (r & 15), so the b128 reads of 16 consecutive rows hit all banks;
+//   V: chunk c of row r at c ^ (8 * ((r >> 2) & 1)), so the two half-waves (rows 4 apart) read
+//      disjoint bank halves.
 
 #include "common.h"
 #include "kernels.h"
@@ -38,28 +47,41 @@ namespace sa {
 
 namespace {
 
-template <int D, int NSPLIT, int BIAS>
-__global__ __launch_bounds__(256) void flash_mfma_kernel(AttnParams p, int q_tiles) {
-  constexpr int QG = 4 / NSPLIT;       // query groups (of 32) per workgroup
-  constexpr int QT = 32 * QG;          // queries per workgroup
-  constexpr int KT = 32 * NSPLIT;      // keys staged per step
-  constexpr int KSTR = D + 4;
-  constexpr int VSTR = D + 8;
-  constexpr int QREG = D / 2;          // Q values per lane
-  constexpr int NDB = D / 32;          // 32-dim output tiles
-  constexpr int F4_ROW = D / 4;        // float4 per row
-  constexpr int NL = KT * F4_ROW / 256;  // float4 loads per thread per tensor per step
-  static_assert(NL * 256 == KT * F4_ROW, "tile must split evenly over 256 threads");
-  constexpr int RB = QT + KT - 1;      // relative-bias entries needed per step
-  constexpr int MSTRIDE = 16 * NDB + 2;  // merge record per lane: O tiles, m, l
-  constexpr int LDS_KV = KT * (KSTR + VSTR);
-  constexpr int LDS_MERGE = (NSPLIT - 1) * QG * 64 * MSTRIDE;
-  constexpr int LDS_FLOATS = LDS_KV > LDS_MERGE ? LDS_KV : LDS_MERGE;
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) const void global_void_t;
 
-  __shared__ __attribute__((aligned(16))) float lds[LDS_FLOATS];
-  __shared__ float lds_rb[BIAS == BIAS_RELPOS ? RB : 1];
-  float* const lds_k = lds;
-  float* const lds_v = lds + KT * KSTR;
+// Moves 16 bytes per lane from global memory to LDS: lane i writes lds_wave_base + 16*i.
+__device__ __forceinline__ void load_to_lds16(const float* src, float* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)lds_wave_base, 16, 0, 0);
+}
+
+constexpr float kRescaleSlack = 8.f;  // log2 units: p stays <= 256 between rescales
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+template <int D, int NSPLIT, int BIAS, int MASK>
+__global__ __launch_bounds__(256) void flash_mfma_kernel(AttnParams p, int q_tiles) {
+  constexpr int QG = 4 / NSPLIT;         // query groups (of 32) per workgroup
+  constexpr int QT = 32 * QG;            // queries per workgroup
+  constexpr int KT = 32 * NSPLIT;        // keys staged per step
+  constexpr int QREG = D / 2;            // Q values per lane
+  constexpr int NDB = D / 32;            // 32-dim output tiles
+  constexpr int CPR = D / 4;             // 16-byte chunks per row
+  constexpr int TILE = KT * D;           // floats per tensor per stage
+  constexpr int NI = KT * CPR / 256;     // LDS-DMA instructions per thread per tensor per step
+  static_assert(NI * 256 == KT * CPR, "tile must split evenly over 256 threads");
+  constexpr int RB = QT + KT - 1;        // relative-bias entries needed per step
+  constexpr int MSTRIDE = 16 * NDB + 2;  // merge record per lane: O tiles, m, l
+  static_assert((NSPLIT - 1) * QG * 64 * MSTRIDE <= 4 * TILE, "merge records must fit in the tiles");
+
+  __shared__ __attribute__((aligned(16))) float lds[2 * 2 * TILE];  // [stage][K tile, V tile]
+  __shared__ float lds_rb[BIAS == BIAS_RELPOS ? 2 * RB : 1];         // [stage][relative bias]
+  __shared__ float lds_km[MASK == MASK_KEY_MASK ? 2 * KT : 1];       // [stage][0 or -inf per key]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -79,13 +101,13 @@ __global__ __launch_bounds__(256) void flash_mfma_kernel(AttnParams p, int q_til
   const bool q_valid = qi < p.Lq;
 
   int kv_len = p.Lk;
-  if (p.mask_mode == MASK_KEY_LEN) kv_len = min(max(p.key_len[b], 0), p.Lk);
+  if constexpr (MASK == MASK_KEY_LEN) kv_len = min(max(p.key_len[b], 0), p.Lk);
   const int nblk = (kv_len + 31) >> 5;
   const int nstep = (nblk + NSPLIT - 1) / NSPLIT;
-  const bool use_kmask = p.mask_mode == MASK_KEY_MASK;
+  constexpr bool use_kmask = MASK == MASK_KEY_MASK;
   const uint8_t* kmask = use_kmask ? p.key_mask + (int64_t)b * p.smask : nullptr;
 
-  // ---- Q into registers: lane holds Q[qi][half*D/2 + s], s = 0..D/2-1
+  // ---- Q into registers, pre-scaled: lane holds scale*log2(e)*Q[qi][half*D/2 + s]
   float qr[QREG];
   {
     const float* src = p.q + p.q_off + (int64_t)b * p.sq + (int64_t)qi * p.ldq + h * D + half * (D / 2);
@@ -93,35 +115,32 @@ __global__ __launch_bounds__(256) void flash_mfma_kernel(AttnParams p, int q_til
     for (int i = 0; i < QREG / 4; ++i) {
       f32x4 x = {0.f, 0.f, 0.f, 0.f};
       if (q_valid) x = *reinterpret_cast<const f32x4*>(src + 4 * i);
-      qr[4 * i + 0] = x[0];
-      qr[4 * i + 1] = x[1];
-      qr[4 * i + 2] = x[2];
-      qr[4 * i + 3] = x[3];
+      qr[4 * i + 0] = x[0] * p.scale_log2;
+      qr[4 * i + 1] = x[1] * p.scale_log2;
+      qr[4 * i + 2] = x[2] * p.scale_log2;
+      qr[4 * i + 3] = x[3] * p.scale_log2;
     }
   }
 
   const float* kbase = p.k + p.k_off + (int64_t)b * p.sk + h * D;
   const float* vbase = p.v + p.v_off + (int64_t)b * p.sv + h * D;
 
-  // ---- K/V staging: thread t moves float4 #(n*256 + t) of the KT x D tile (row-major)
-  f32x4 pk[NL], pv[NL];
-  float prb = 0.f;
-  auto load_step = [&](int step) {
+  // ---- issue the HBM -> LDS copy of step `step` into stage `buf`
+  auto issue = [&](int step, int buf) {
+    float* kt = lds + buf * 2 * TILE;
+    float* vt = kt + TILE;
     const int key0 = step * KT;
 #pragma unroll
-    for (int n = 0; n < NL; ++n) {
-      const int idx = n * 256 + tid;
-      const int row = idx / F4_ROW;
-      const int c4 = idx % F4_ROW;
-      const int key = key0 + row;
-      f32x4 zk = {0.f, 0.f, 0.f, 0.f};
-      f32x4 zv = zk;
-      if (key < kv_len) {
-        zk = *reinterpret_cast<const f32x4*>(kbase + (int64_t)key * p.ldk + 4 * c4);
-        zv = *reinterpret_cast<const f32x4*>(vbase + (int64_t)key * p.ldv + 4 * c4);
-      }
-      pk[n] = zk;
-      pv[n] = zv;
+    for (int n = 0; n < NI; ++n) {
+      const int blk64 = n * 4 + wave;        // 64-chunk (1 KiB) block of the tile
+      const int pc_all = blk64 * 64 + lane;  // physical chunk this lane fills
+      const int row = pc_all / CPR;
+      const int pc = pc_all % CPR;
+      const int key = min(key0 + row, kv_len - 1);
+      const int ck = pc ^ (row & 15);
+      const int cv = pc ^ (((row >> 2) & 1) << 3);
+      load_to_lds16(kbase + (int64_t)key * p.ldk + 4 * ck, kt + blk64 * 256);
+      load_to_lds16(vbase + (int64_t)key * p.ldv + 4 * cv, vt + blk64 * 256);
     }
     if constexpr (BIAS == BIAS_RELPOS) {
       // entry e covers LUT index key0 - (q0 + QT - 1) + (Lq - 1) + e
@@ -133,120 +152,122 @@ __global__ __launch_bounds__(256) void flash_mfma_kernel(AttnParams p, int q_til
           bucket = min(max(bucket, 0), p.num_buckets - 1);
           val = p.bias[bucket * p.H + h] * kLog2e;
         }
-        prb = val;
+        lds_rb[buf * RB + tid] = val;
       }
     }
-  };
-  auto store_step = [&]() {
-#pragma unroll
-    for (int n = 0; n < NL; ++n) {
-      const int idx = n * 256 + tid;
-      const int row = idx / F4_ROW;
-      const int c4 = idx % F4_ROW;
-      *reinterpret_cast<f32x4*>(lds_k + row * KSTR + 4 * c4) = pk[n];
-      *reinterpret_cast<f32x4*>(lds_v + row * VSTR + 4 * c4) = pv[n];
-    }
-    if constexpr (BIAS == BIAS_RELPOS) {
-      if (tid < RB) lds_rb[tid] = prb;
+    if constexpr (use_kmask) {
+      // additive key mask of the step, read unconditionally at a clamped index (branch-free)
+      if (tid < KT) {
+        const int key = key0 + tid;
+        const uint8_t byte = kmask[min(key, p.Lk - 1)];
+        lds_km[buf * KT + tid] = (key < kv_len && byte != 0) ? 0.f : -INFINITY;
+      }
     }
   };
 
   f32x16 oacc[NDB];
 #pragma unroll
-  for (int t = 0; t < NDB; ++t) oacc[t] = f32x16{0.f};
+  for (int t = 0; t < NDB; ++t) oacc[t] = zero16();
   float m = kMaxSeed;
   float l = 0.f;
 
-  if (nstep > 0) {
-    load_step(0);
-    store_step();
-  }
+  if (nstep > 0) issue(0, 0);
 
   for (int step = 0; step < nstep; ++step) {
+    const int buf = step & 1;
+    // stage `buf` has landed for this thread; the barrier makes it whole, and every wave has
+    // finished reading stage buf^1 (the previous step), which the next issue overwrites
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (step + 1 < nstep) load_step(step + 1);
+    if (step + 1 < nstep) issue(step + 1, buf ^ 1);
     const int blk = step * NSPLIT + ks;
     if (blk < nblk) {
       const int k0 = blk * 32;
-      // ---- S^T = K Q^T for 32 keys x 32 queries
-      f32x16 s = f32x16{0.f};
-      const float* krow = lds_k + (ks * 32 + col) * KSTR + half * (D / 2);
+      const float* kt = lds + buf * 2 * TILE;
+      const float* vt = kt + TILE;
+      // ---- u^T = K (scaled Q)^T for 32 keys x 32 queries
+      f32x16 s = zero16();
+      const float* krow = kt + (ks * 32 + col) * D;
+      const int ksw = col & 15;
 #pragma unroll
       for (int i = 0; i < QREG / 4; ++i) {
-        const f32x4 kv = *reinterpret_cast<const f32x4*>(krow + 4 * i);
+        const int c = (half * (CPR / 2) + i) ^ ksw;
+        const f32x4 kv = *reinterpret_cast<const f32x4*>(krow + 4 * c);
         s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[0], qr[4 * i + 0], s, 0, 0, 0);
         s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[1], qr[4 * i + 1], s, 0, 0, 0);
         s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[2], qr[4 * i + 2], s, 0, 0, 0);
         s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[3], qr[4 * i + 3], s, 0, 0, 0);
       }
 
-      // ---- scores in the base-2 domain, bias and masks
+      // ---- bias and masks
       float u[16];
-      if constexpr (BIAS == BIAS_NONE) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) u[r] = s[r] * p.scale_log2;
-      } else if constexpr (BIAS == BIAS_RELPOS) {
+      for (int r = 0; r < 16; ++r) u[r] = s[r];
+      if constexpr (BIAS == BIAS_RELPOS) {
         // rb entry for (key, qi): key - qi + (q0 + QT - 1) - step*KT
-        const int rb0 = k0 - step * KT + 4 * half - qi + q0 + QT - 1;
+        const float* rb = lds_rb + buf * RB + (k0 - step * KT + 4 * half - qi + q0 + QT - 1);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int e = rb0 + 8 * (r >> 2) + (r & 3);
-          u[r] = fmaf(s[r], p.scale_log2, lds_rb[e]);
-        }
-      } else {  // BIAS_DENSE
-        const float* brow = p.bias + (int64_t)b * p.sbias + ((int64_t)h * p.Lq + (q_valid ? qi : 0)) * p.Lk;
+        for (int r = 0; r < 16; ++r) u[r] += rb[8 * (r >> 2) + (r & 3)];
+      } else if constexpr (BIAS == BIAS_DENSE) {
+        // unconditional loads at clamped indices; out-of-range keys are masked below
+        const float* brow = p.bias + (int64_t)b * p.sbias + ((int64_t)h * p.Lq + min(qi, p.Lq - 1)) * p.Lk;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = k0 + 8 * (r >> 2) + 4 * half + (r & 3);
-          const float bv = (q_valid && key < kv_len) ? brow[key] * kLog2e : 0.f;
-          u[r] = fmaf(s[r], p.scale_log2, bv);
+          u[r] = fmaf(brow[min(key, p.Lk - 1)], kLog2e, u[r]);
         }
       }
-      if (k0 + 32 > kv_len || use_kmask) {
+      if constexpr (use_kmask) {
+        // the staged additive mask also covers keys past Lk
+        const float* km = lds_km + buf * KT + (k0 - step * KT) + 4 * half;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) u[r] += km[8 * (r >> 2) + (r & 3)];
+      } else if (k0 + 32 > kv_len) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = k0 + 8 * (r >> 2) + 4 * half + (r & 3);
-          bool keep = key < kv_len;
-          if (use_kmask && keep) keep = kmask[key] != 0;
-          if (!keep) u[r] = -INFINITY;
+          u[r] = key < kv_len ? u[r] : -INFINITY;
         }
       }
 
-      // ---- online softmax
+      // ---- online softmax with a lazily moved reference
       float mb = u[0];
 #pragma unroll
       for (int r = 1; r < 16; ++r) mb = fmaxf(mb, u[r]);
       mb = max_with_partner(mb);
-      const float m_new = fmaxf(m, mb);
-      const float alpha = fast_exp2(m - m_new);
-      m = m_new;
+      if (__builtin_amdgcn_ballot_w64(mb > m + kRescaleSlack) != 0) {
+        const float m_new = fmaxf(m, mb);
+        const float alpha = fast_exp2(m - m_new);
+        m = m_new;
+        l *= alpha;
+#pragma unroll
+        for (int t = 0; t < NDB; ++t) oacc[t] *= alpha;
+      }
       float ps = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        u[r] = fast_exp2(u[r] - m_new);
+        u[r] = fast_exp2(u[r] - m);
         ps += u[r];
       }
-      l = fmaf(l, alpha, ps);
-#pragma unroll
-      for (int t = 0; t < NDB; ++t) oacc[t] *= alpha;
+      l += ps;
 
-      // ---- O^T += V^T P^T
-      const float* vcol = lds_v + (ks * 32 + 4 * half) * VSTR + col;
+      // ---- O^T += V^T P^T; V element (row, 32t + col) sits in chunk (8t + col/4) ^ 8*half
+      const float* vrow = vt + (ks * 32 + 4 * half) * D + col;
 #pragma unroll
       for (int t = 0; t < NDB; ++t) {
+        const float* vcol = vrow + 32 * (t ^ half);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float vv = vcol[(8 * (r >> 2) + (r & 3)) * VSTR + 32 * t];
+          const float vv = vcol[(8 * (r >> 2) + (r & 3)) * D];
           oacc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, u[r], oacc[t], 0, 0, 0);
         }
       }
     }
-    __syncthreads();
-    if (step + 1 < nstep) store_step();
   }
 
   // ---- merge the key splits: waves ks > 0 publish (O, m, l), wave ks == 0 combines
   if constexpr (NSPLIT > 1) {
+    __syncthreads();  // every wave is done with the tiles the records overwrite
     float* rec = lds + ((ks - 1) * QG + qg) * 64 * MSTRIDE + lane;
     if (ks > 0) {
 #pragma unroll
@@ -300,27 +321,35 @@ __global__ __launch_bounds__(256) void flash_mfma_kernel(AttnParams p, int q_til
   }
 }
 
+template <int D, int NSPLIT, int BIAS, int MASK>
+hipError_t launch_one(const AttnParams& p, int q_tiles, dim3 grid, hipStream_t stream) {
+  hipLaunchKernelGGL((flash_mfma_kernel<D, NSPLIT, BIAS, MASK>), grid, dim3(256), 0, stream, p, q_tiles);
+  return hipGetLastError();
+}
+
+template <int D, int NSPLIT, int BIAS>
+hipError_t launch_mask(const AttnParams& p, int q_tiles, dim3 grid, hipStream_t stream) {
+  switch (p.mask_mode) {
+    case MASK_NONE: return launch_one<D, NSPLIT, BIAS, MASK_NONE>(p, q_tiles, grid, stream);
+    case MASK_KEY_LEN: return launch_one<D, NSPLIT, BIAS, MASK_KEY_LEN>(p, q_tiles, grid, stream);
+    case MASK_KEY_MASK: return launch_one<D, NSPLIT, BIAS, MASK_KEY_MASK>(p, q_tiles, grid, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 template <int D, int NSPLIT>
 hipError_t launch_split(const AttnParams& p, hipStream_t stream) {
   constexpr int QT = 32 * (4 / NSPLIT);
   const int q_tiles = (p.Lq + QT - 1) / QT;
   const int64_t n = (int64_t)p.B * p.H * q_tiles;
   if (n > 0x7fffffff) return hipErrorInvalidConfiguration;
-  const dim3 grid((unsigned)n), block(256);
+  const dim3 grid((unsigned)n);
   switch (p.bias_mode) {
-    case BIAS_NONE:
-      hipLaunchKernelGGL((flash_mfma_kernel<D, NSPLIT, BIAS_NONE>), grid, block, 0, stream, p, q_tiles);
-      break;
-    case BIAS_DENSE:
-      hipLaunchKernelGGL((flash_mfma_kernel<D, NSPLIT, BIAS_DENSE>), grid, block, 0, stream, p, q_tiles);
-      break;
-    case BIAS_RELPOS:
-      hipLaunchKernelGGL((flash_mfma_kernel<D, NSPLIT, BIAS_RELPOS>), grid, block, 0, stream, p, q_tiles);
-      break;
-    default:
-      return hipErrorInvalidValue;
+    case BIAS_NONE: return launch_mask<D, NSPLIT, BIAS_NONE>(p, q_tiles, grid, stream);
+    case BIAS_DENSE: return launch_mask<D, NSPLIT, BIAS_DENSE>(p, q_tiles, grid, stream);
+    case BIAS_RELPOS: return launch_mask<D, NSPLIT, BIAS_RELPOS>(p, q_tiles, grid, stream);
+    default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 }  // namespace

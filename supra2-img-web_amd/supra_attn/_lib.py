@@ -39,6 +39,7 @@ SIGNATURES = {
     "sa_free": (c_int, [c_void_p]),
     "sa_memcpy_h2d": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
     "sa_memcpy_d2h": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
+    "sa_memcpy_d2d": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
     "sa_memset": (c_int, [c_void_p, c_int, c_size_t, c_void_p]),
     "sa_stream_create": (c_int, [POINTER(c_void_p)]),
     "sa_stream_destroy": (c_int, [c_void_p]),
