@@ -1,0 +1,113 @@
+// GPU run of the JS shim in the exact call forms of the reference callers; outputs go back to
+// Python for the oracle comparison.
+// Usage: node tests/node/ops_gpu.js <dir>   (reads <dir>/manifest.json and <dir>/*.bin)
+"use strict";
+
+var fs = require("fs");
+var path = require("path");
+
+var sa = require(path.join(__dirname, "..", "..", "supra2-img-web_amd", "js", "index.js"));
+
+var dir = process.argv[2];
+var manifest = JSON.parse(fs.readFileSync(path.join(dir, "manifest.json"), "utf8"));
+
+function loadBin(name, Type) {
+  var b = fs.readFileSync(path.join(dir, name));
+  var T = Type || Float32Array;
+  return new T(b.buffer.slice(b.byteOffset, b.byteOffset + b.byteLength));
+}
+
+function saveBin(name, arr) {
+  fs.writeFileSync(path.join(dir, name), Buffer.from(arr.buffer, arr.byteOffset, arr.byteLength));
+}
+
+var forms = {
+  // app/models/dit.js:169-173: one launch per sample on the packed qkv buffer
+  dit_self_loop: function (gpu, c) {
+    var D = 576, TOK = 256;
+    var qkv = gpu.fromArray(loadBin(c.qkv), [c.B * TOK, 3 * D]);
+    var a = gpu.empty([c.B * TOK, D]);
+    for (var b = 0; b < c.B; b++) {
+      var r = b * TOK * 3 * D;
+      sa.attention(gpu, { q: qkv, k: qkv, v: qkv, Lq: TOK, Lk: TOK, H: 9, D: 64, ldq: 3 * D, ldk: 3 * D, ldv: 3 * D,
+        qOff: r, kOff: r + D, vOff: r + 2 * D, oOff: b * TOK * D, out: a });
+    }
+    qkv.release();
+    return a;
+  },
+  // the same batch in one launch with batch strides
+  dit_self_batched: function (gpu, c) {
+    var D = 576, TOK = 256;
+    var qkv = gpu.fromArray(loadBin(c.qkv), [c.B * TOK, 3 * D]);
+    var a = sa.attention(gpu, { B: c.B, q: qkv, k: qkv, v: qkv, Lq: TOK, Lk: TOK, H: 9, D: 64, ldq: 3 * D,
+      ldk: 3 * D, ldv: 3 * D, kOff: D, vOff: 2 * D, sq: TOK * 3 * D, sk: TOK * 3 * D, sv: TOK * 3 * D,
+      so: TOK * D });
+    qkv.release();
+    return a;
+  },
+  // app/models/dit.js:181-185: per-sample k|v buffers [L_b, 1152] at their true length
+  dit_cross_loop: function (gpu, c) {
+    var D = 576, TOK = 256;
+    var q = gpu.fromArray(loadBin(c.q), [c.B * TOK, D]);
+    var out = gpu.empty([c.B * TOK, D]);
+    for (var b = 0; b < c.B; b++) {
+      var kv = gpu.fromArray(loadBin(c.kv[b]), [c.L[b], 2 * D]);
+      sa.attention(gpu, { q: q, k: kv, v: kv, Lq: TOK, Lk: c.L[b], H: 9, D: 64, ldq: D, ldk: 2 * D, ldv: 2 * D,
+        qOff: b * TOK * D, kOff: 0, vOff: D, oOff: b * TOK * D, out: out });
+      kv.release();
+    }
+    q.release();
+    return out;
+  },
+  // app/models/t5.js:73-80: dense [H, L, L] position bias, scale 1 (bias built on the device)
+  t5_dense: function (gpu, c) {
+    var q = gpu.fromArray(loadBin(c.q), [c.L, 768]);
+    var k = gpu.fromArray(loadBin(c.k), [c.L, 768]);
+    var v = gpu.fromArray(loadBin(c.v), [c.L, 768]);
+    var bias = sa.positionBias(gpu, loadBin(c.table), 32, 12, c.L);
+    var a = sa.attention(gpu, { q: q, k: k, v: v, Lq: c.L, Lk: c.L, H: 12, D: 64, ldq: 768, ldk: 768, ldv: 768,
+      scale: 1, bias: bias });
+    q.release(); k.release(); v.release(); bias.release();
+    return a;
+  },
+  // the relative-position table gathered in-kernel plus a key-padding mask
+  t5_relpos_mask: function (gpu, c) {
+    var q = gpu.fromArray(loadBin(c.q), [c.L, 768]);
+    var k = gpu.fromArray(loadBin(c.k), [c.L, 768]);
+    var v = gpu.fromArray(loadBin(c.v), [c.L, 768]);
+    var rp = sa.relposBias(gpu, loadBin(c.table), 32, 12, c.L, c.L);
+    var km = gpu.fromArray(loadBin(c.mask, Uint8Array), [1, c.L]);
+    var a = sa.attention(gpu, { q: q, k: k, v: v, Lq: c.L, Lk: c.L, H: 12, D: 64, ldq: 768, ldk: 768, ldv: 768,
+      scale: 1, relpos: rp, keyMask: km });
+    return a;
+  },
+  // app/models/vae.js:86: single head, D = C = 512, default scale
+  vae: function (gpu, c) {
+    var q = gpu.fromArray(loadBin(c.q), [c.L, 512]);
+    var k = gpu.fromArray(loadBin(c.k), [c.L, 512]);
+    var v = gpu.fromArray(loadBin(c.v), [c.L, 512]);
+    return sa.attention(gpu, { q: q, k: k, v: v, Lq: c.L, Lk: c.L, H: 1, D: 512, ldq: 512, ldk: 512, ldv: 512 });
+  },
+};
+
+sa.GPU.create().then(function (gpu) {
+  var chain = Promise.resolve();
+  manifest.cases.forEach(function (c) {
+    chain = chain.then(function () {
+      process.stdout.write("[node case] " + c.name + "\n");
+      var out = forms[c.form](gpu, c);
+      return gpu.sync().then(function () {
+        return gpu.read(out);
+      }).then(function (data) {
+        saveBin(c.name + ".out.bin", data);
+        out.release();
+      });
+    });
+  });
+  return chain;
+}).then(function () {
+  process.stdout.write("node: all cases ran\n");
+}, function (e) {
+  process.stderr.write("node failure: " + (e.code || e.name) + ": " + e.message + "\n");
+  process.exit(1);
+});

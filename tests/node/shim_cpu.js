@@ -1,0 +1,185 @@
+// CPU checks of the JS binding (no GPU): the addon loads under Node, exports its functions and
+// constants, computes T5 buckets, rejects invalid calls with C ABI status codes; the shim maps the
+// reference call forms (app/models/dit.js:172, dit.js:184, t5.js:80, vae.js:86) onto sa_attn_args
+// as expected, and the buffer pool reuses released buffers.
+// Usage: node tests/node/shim_cpu.js <expected-buckets.json>
+"use strict";
+
+var assert = require("assert");
+var fs = require("fs");
+var path = require("path");
+
+var root = path.join(__dirname, "..", "..", "supra2-img-web_amd", "js");
+var sa = require(path.join(root, "index.js"));
+var device = require(path.join(root, "device.js"));
+var native = device.loadNative();
+
+var checks = 0;
+function check(name, fn) {
+  fn();
+  checks++;
+  process.stdout.write("ok " + name + "\n");
+}
+
+check("addon exports", function () {
+  ["attention", "kernelName", "version", "deviceCount", "malloc", "free", "upload", "download", "memset", "sync",
+    "bucketLut", "positionBias", "eventCreate", "eventRecord", "eventElapsed", "eventDestroy"].forEach(function (f) {
+    assert.strictEqual(typeof native[f], "function", f);
+  });
+  assert.strictEqual(native.version(), 1);
+  assert.strictEqual(native.SA_BIAS_RELPOS, 2);
+  assert.strictEqual(native.SA_MASK_KEY_MASK, 2);
+});
+
+check("bucket LUT matches the oracle's", function () {
+  var expected = JSON.parse(fs.readFileSync(process.argv[2], "utf8"));
+  var lut = native.bucketLut(expected.Lq, expected.Lk, 32, 128, true);
+  assert.strictEqual(lut.length, expected.lut.length);
+  for (var i = 0; i < lut.length; i++) assert.strictEqual(lut[i], expected.lut[i], "index " + i);
+  expected.singles.forEach(function (p) {
+    assert.strictEqual(sa.relativeBucket(p[0], 32, 128, native), p[1], "rel " + p[0]);
+  });
+});
+
+check("invalid calls throw with a status code before touching the device", function () {
+  assert.throws(function () {
+    native.attention({ B: 1, H: 1, D: 64, Lq: 4, Lk: 4, ldq: 64, ldk: 64, ldv: 64, scale: 1 });
+  }, function (e) {
+    return e.code === "SA_ERR_INVALID" && /non-NULL/.test(e.message);
+  });
+  assert.throws(function () {
+    native.attention({ H: 2, D: 64, Lq: "x" });
+  }, function (e) {
+    return e.code === "SA_ERR_INVALID";
+  });
+  assert.throws(function () {
+    native.bucketLut(0, 4, 32, 128, true);
+  }, function (e) {
+    return e.code === "SA_ERR_INVALID";
+  });
+});
+
+// a fake addon: records calls, hands out numbered buffers
+function fakeNative() {
+  var n = 0;
+  return {
+    calls: [],
+    mallocs: 0,
+    deviceCount: function () { return 1; },
+    malloc: function (bytes) { this.mallocs++; return { id: ++n, bytes: bytes }; },
+    free: function () {},
+    upload: function () {},
+    download: function () {},
+    sync: function () {},
+    attention: function (a) { this.calls.push(a); },
+    kernelName: function () { return "fake"; },
+    bucketLut: native.bucketLut,
+  };
+}
+
+function makeGpu() {
+  var f = fakeNative();
+  return { f: f, gpu: new device.GPU(f) };
+}
+
+check("DiT self-attention form (dit.js:172)", function () {
+  var g = makeGpu();
+  var D = 576, TOK = 256;
+  var qkv = g.gpu.empty([2 * TOK, 3 * D]);
+  var a = g.gpu.empty([2 * TOK, D]);
+  for (var b = 0; b < 2; b++) {
+    var r = b * TOK * 3 * D;
+    var ret = sa.attention(g.gpu, { q: qkv, k: qkv, v: qkv, Lq: TOK, Lk: TOK, H: 9, D: 64, ldq: 3 * D, ldk: 3 * D,
+      ldv: 3 * D, qOff: r, kOff: r + D, vOff: r + 2 * D, oOff: b * TOK * D, out: a });
+    assert.strictEqual(ret, a);
+  }
+  assert.strictEqual(g.f.calls.length, 2);
+  var c = g.f.calls[1];
+  assert.strictEqual(c.B, 1);
+  assert.strictEqual(c.qOff, TOK * 3 * D);
+  assert.strictEqual(c.kOff, TOK * 3 * D + D);
+  assert.strictEqual(c.vOff, TOK * 3 * D + 2 * D);
+  assert.strictEqual(c.oOff, TOK * D);
+  assert.strictEqual(c.ldo, D);
+  assert.strictEqual(c.scale, 1 / 8);
+  assert.strictEqual(c.q, qkv.buf);
+  assert.strictEqual(c.out, a.buf);
+  assert.strictEqual(c.biasMode, 0);
+  assert.strictEqual(c.maskMode, 0);
+});
+
+check("DiT cross-attention form (dit.js:184) and its batched padded form", function () {
+  var g = makeGpu();
+  var q = g.gpu.empty([512, 576]);
+  var kv = g.gpu.empty([77, 1152]);
+  var c = g.gpu.empty([512, 576]);
+  sa.attention(g.gpu, { q: q, k: kv, v: kv, Lq: 256, Lk: 77, H: 9, D: 64, ldq: 576, ldk: 1152, ldv: 1152,
+    qOff: 256 * 576, kOff: 0, vOff: 576, oOff: 256 * 576, out: c });
+  var a = g.f.calls[0];
+  assert.strictEqual(a.Lk, 77);
+  assert.strictEqual(a.vOff, 576);
+  assert.strictEqual(a.ldk, 1152);
+  var kvp = g.gpu.empty([2 * 128, 1152]);
+  var kl = g.gpu.fromArray(new Int32Array([77, 1]), [2]);
+  sa.attention(g.gpu, { B: 2, q: q, k: kvp, v: kvp, Lq: 256, Lk: 128, H: 9, D: 64, ldq: 576, ldk: 1152, ldv: 1152,
+    vOff: 576, sq: 256 * 576, sk: 128 * 1152, sv: 128 * 1152, so: 256 * 576, keyLen: kl, out: c });
+  a = g.f.calls[1];
+  assert.strictEqual(a.B, 2);
+  assert.strictEqual(a.maskMode, 1);
+  assert.strictEqual(a.keyLen, kl.buf);
+  assert.strictEqual(a.sk, 128 * 1152);
+  assert.strictEqual(kl.dtype, "i32");
+});
+
+check("T5 form (t5.js:80): scale 1, dense bias; relpos + key-mask extension", function () {
+  var g = makeGpu();
+  var q = g.gpu.empty([128, 768]);
+  var bias = g.gpu.empty([12, 128, 128]);
+  var out = sa.attention(g.gpu, { q: q, k: q, v: q, Lq: 128, Lk: 128, H: 12, D: 64, ldq: 768, ldk: 768, ldv: 768,
+    scale: 1, bias: bias });
+  assert.deepStrictEqual(out.shape, [128, 768]);
+  var a = g.f.calls[0];
+  assert.strictEqual(a.scale, 1);
+  assert.strictEqual(a.biasMode, 1);
+  assert.strictEqual(a.bias, bias.buf);
+  assert.strictEqual(a.sbias, 0);
+  var rp = sa.relposBias(g.gpu, new Float32Array(32 * 12), 32, 12, 128, 128);
+  assert.deepStrictEqual(rp.lut.shape, [255]);
+  var km = g.gpu.fromArray(new Uint8Array(128).fill(1), [1, 128]);
+  sa.attention(g.gpu, { q: q, k: q, v: q, Lq: 128, Lk: 128, H: 12, D: 64, ldq: 768, ldk: 768, ldv: 768, scale: 1,
+    relpos: rp, keyMask: km });
+  a = g.f.calls[1];
+  assert.strictEqual(a.biasMode, 2);
+  assert.strictEqual(a.numBuckets, 32);
+  assert.strictEqual(a.bucketLut, rp.lut.buf);
+  assert.strictEqual(a.maskMode, 2);
+  assert.strictEqual(a.smask, 128);
+});
+
+check("VAE form (vae.js:86): one head, D = 512, default scale", function () {
+  var g = makeGpu();
+  var q = g.gpu.empty([1024, 512]);
+  sa.attention(g.gpu, { q: q, k: q, v: q, Lq: 1024, Lk: 1024, H: 1, D: 512, ldq: 512, ldk: 512, ldv: 512 });
+  var a = g.f.calls[0];
+  assert.strictEqual(a.scale, 1 / Math.sqrt(512));
+  assert.strictEqual(a.ldo, 512);
+  assert.strictEqual(a.so, 512 * 1024);
+});
+
+check("released tensors are reused and cannot be passed again", function () {
+  var g = makeGpu();
+  var t = g.gpu.empty([1000]);
+  var buf = t.buf;
+  t.release();
+  assert.strictEqual(t.buf, null);
+  var u = g.gpu.empty([999]);
+  assert.strictEqual(u.buf, buf);
+  assert.strictEqual(g.f.mallocs, 1);
+  assert.throws(function () {
+    sa.attention(g.gpu, { q: t, k: u, v: u, Lq: 1, Lk: 1, H: 1, D: 64, ldq: 64, ldk: 64, ldv: 64 });
+  }, /released/);
+  assert.strictEqual(device.BufferPool.round(1), 256);
+  assert.strictEqual(device.BufferPool.round(5000), 5120);
+});
+
+process.stdout.write("all " + checks + " checks passed\n");

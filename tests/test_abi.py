@@ -1,0 +1,173 @@
+"""The C ABI boundary on the CPU: the library loads, exports every symbol include/supra_attn.h
+declares, lays out sa_attn_args as the Python mirror does, and rejects invalid calls before any
+launch (no GPU needed: validation never touches the pointers it is given)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from oracle import t5_bucket as tb
+from supra_attn import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "supra_attn.h")
+FAKE = 0x7F0000000000  # a device-looking address; validation only compares addresses
+
+
+def header_functions() -> list[str]:
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\**\s*(sa_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = _lib.load()
+    names = header_functions()
+    assert len(names) >= 20
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in the header but not exported"
+    assert sorted(_lib.SIGNATURES) == names, "ctypes bindings drift from the header"
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\bT (sa_\w+)", out))
+    assert exported == set(names), f"exported but undeclared: {exported - set(names)}"
+
+
+def test_version_and_constants():
+    lib = _lib.load()
+    assert lib.sa_version() == 1
+    text = open(HEADER).read()
+    for name in ("SA_OK", "SA_ERR_INVALID", "SA_ERR_UNSUPPORTED", "SA_ERR_HIP", "SA_ERR_ALIAS", "SA_BIAS_NONE",
+                 "SA_BIAS_DENSE", "SA_BIAS_RELPOS", "SA_MASK_NONE", "SA_MASK_KEY_LEN", "SA_MASK_KEY_MASK"):
+        m = re.search(rf"#define {name} \(?(-?\d+)\)?", text)
+        assert m and int(m.group(1)) == getattr(_lib, name), name
+
+
+def test_struct_layout_matches_c(tmp_path):
+    fields = [f[0] for f in _lib.AttnArgs._fields_]
+    src = tmp_path / "layout.c"
+    body = "\n".join(f'  printf("{f} %zu\\n", offsetof(sa_attn_args, {f}));' for f in fields)
+    src.write_text(f'#include <stdio.h>\n#include <stddef.h>\n#include "supra_attn.h"\nint main(void) {{\n'
+                   f'  printf("sizeof %zu\\n", sizeof(sa_attn_args));\n{body}\n  return 0;\n}}\n')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", f"-I{os.path.dirname(HEADER)}", str(src), "-o", str(exe)], check=True)
+    lines = dict(ln.split() for ln in subprocess.run([str(exe)], capture_output=True, text=True).stdout.splitlines())
+    assert int(lines["sizeof"]) == ctypes.sizeof(_lib.AttnArgs)
+    for f in fields:
+        assert int(lines[f]) == getattr(_lib.AttnArgs, f).offset, f
+
+
+def good_args(**over):
+    kw = dict(B=2, H=9, D=64, Lq=256, Lk=256, q=FAKE, k=FAKE, v=FAKE, o=FAKE + (1 << 32), q_off=0, k_off=576,
+              v_off=1152, ldq=1728, ldk=1728, ldv=1728, ldo=576, sq=256 * 1728, sk=256 * 1728, sv=256 * 1728,
+              so=256 * 576, scale=0.125)
+    kw.update(over)
+    return _lib.AttnArgs(**kw)
+
+
+def rc_of(args):
+    return _lib.load().sa_attention_f32(ctypes.byref(args), None)
+
+
+def test_valid_call_selects_mfma_kernel():
+    assert _lib.kernel_name(good_args()) == "flash_mfma_d64_split4"
+    assert _lib.kernel_name(good_args(B=64, o=FAKE + (1 << 36), sq=256 * 1728)) == "flash_mfma_d64"
+    assert _lib.kernel_name(good_args(B=16, o=FAKE + (1 << 36))) == "flash_mfma_d64_split2"
+    assert _lib.kernel_name(good_args(D=128, H=4, ldo=512, so=256 * 512)) == "flash_mfma_d128_split2"
+
+
+def test_generic_kernel_for_other_head_dims_and_unaligned_rows():
+    assert _lib.kernel_name(good_args(D=32, ldo=288, so=256 * 288)) == "generic"
+    assert _lib.kernel_name(good_args(q_off=1)) == "generic"
+    assert _lib.kernel_name(good_args(ldq=1729, ldk=1729, ldv=1729)) == "generic"
+    assert _lib.kernel_name(good_args(q=FAKE + 4, k=FAKE + 4, v=FAKE + 4)) == "generic"
+    vae = _lib.AttnArgs(B=1, H=1, D=512, Lq=1024, Lk=1024, q=FAKE, k=FAKE + (1 << 24), v=FAKE + (2 << 24),
+                        o=FAKE + (3 << 24), ldq=512, ldk=512, ldv=512, scale=0.0442)
+    assert _lib.kernel_name(vae) in ("generic", "vae_mfma_d512")
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(struct_size=8), _lib.SA_ERR_INVALID),
+    (dict(B=0), _lib.SA_ERR_INVALID),
+    (dict(H=0), _lib.SA_ERR_INVALID),
+    (dict(Lq=0), _lib.SA_ERR_INVALID),
+    (dict(Lk=0), _lib.SA_ERR_INVALID),
+    (dict(q=0), _lib.SA_ERR_INVALID),
+    (dict(o=0), _lib.SA_ERR_INVALID),
+    (dict(scale=float("nan")), _lib.SA_ERR_INVALID),
+    (dict(scale=float("inf")), _lib.SA_ERR_INVALID),
+    (dict(q_off=-4), _lib.SA_ERR_INVALID),
+    (dict(ldq=500), _lib.SA_ERR_INVALID),
+    (dict(ldo=100), _lib.SA_ERR_INVALID),
+    (dict(so=100), _lib.SA_ERR_INVALID),
+    (dict(sq=-1), _lib.SA_ERR_INVALID),
+    (dict(o=FAKE + 4096), _lib.SA_ERR_ALIAS),
+    (dict(bias_mode=1), _lib.SA_ERR_INVALID),
+    (dict(bias_mode=2, bias=FAKE + (2 << 32)), _lib.SA_ERR_INVALID),
+    (dict(bias_mode=2, bias=FAKE + (2 << 32), bucket_lut=FAKE + (3 << 32)), _lib.SA_ERR_INVALID),
+    (dict(bias_mode=7), _lib.SA_ERR_INVALID),
+    (dict(mask_mode=1), _lib.SA_ERR_INVALID),
+    (dict(mask_mode=2), _lib.SA_ERR_INVALID),
+    (dict(mask_mode=2, key_mask=FAKE + (2 << 32), smask=100), _lib.SA_ERR_INVALID),
+    (dict(mask_mode=9), _lib.SA_ERR_INVALID),
+    (dict(D=2048, ldq=1 << 16, ldk=1 << 16, ldv=1 << 16, ldo=1 << 16, so=256 << 16), _lib.SA_ERR_UNSUPPORTED),
+])
+def test_invalid_calls_are_rejected_before_launch(over, code):
+    args = good_args(**over)
+    if "struct_size" in over:
+        args.struct_size = over["struct_size"]
+    assert rc_of(args) == code
+    msg = _lib.load().sa_last_error().decode()
+    assert msg, "an error must carry a message"
+    assert _lib.load().sa_attention_kernel_name(ctypes.byref(args)) is None
+
+
+def test_null_args_pointer():
+    lib = _lib.load()
+    assert lib.sa_attention_f32(None, None) == _lib.SA_ERR_INVALID
+    assert b"NULL" in lib.sa_last_error()
+
+
+def test_error_message_clears_on_success():
+    lib = _lib.load()
+    assert rc_of(good_args(B=0)) == _lib.SA_ERR_INVALID
+    assert _lib.kernel_name(good_args()) == "flash_mfma_d64_split4"
+    assert lib.sa_last_error() == b""
+
+
+@pytest.mark.parametrize("Lq,Lk", [(1, 1), (128, 128), (7, 300), (300, 7)])
+@pytest.mark.parametrize("bidirectional", [True, False])
+def test_bucket_lut_matches_oracle(Lq, Lk, bidirectional):
+    got = _lib.bucket_lut(Lq, Lk, 32, 128, bidirectional)
+    np.testing.assert_array_equal(got, tb.bucket_lut(Lq, Lk, bidirectional))
+
+
+def test_bucket_lut_other_bucket_counts():
+    for nb, md in ((16, 64), (64, 256), (8, 20)):
+        got = _lib.bucket_lut(50, 60, nb, md, True)
+        np.testing.assert_array_equal(got, tb.bucket_lut(50, 60, True, nb, md))
+
+
+def test_bucket_lut_rejects_bad_arguments():
+    lib = _lib.load()
+    out = (ctypes.c_int32 * 8)()
+    assert lib.sa_t5_bucket_lut(0, 4, 32, 128, 1, out) == _lib.SA_ERR_INVALID
+    assert lib.sa_t5_bucket_lut(4, 4, 2, 128, 1, out) == _lib.SA_ERR_INVALID
+    assert lib.sa_t5_bucket_lut(4, 4, 32, 4, 1, out) == _lib.SA_ERR_INVALID
+    assert lib.sa_t5_bucket_lut(4, 4, 32, 128, 1, None) == _lib.SA_ERR_INVALID
+
+
+def test_device_helpers_reject_null_pointers():
+    lib = _lib.load()
+    assert lib.sa_malloc(None, 16) == _lib.SA_ERR_INVALID
+    assert lib.sa_memcpy_h2d(None, None, 16, None) == _lib.SA_ERR_INVALID
+    assert lib.sa_memcpy_d2h(None, None, 16, None) == _lib.SA_ERR_INVALID
+    assert lib.sa_memcpy_d2d(None, None, 16, None) == _lib.SA_ERR_INVALID
+    assert lib.sa_event_elapsed_ms(None, None, None) == _lib.SA_ERR_INVALID
+    assert lib.sa_t5_position_bias(None, None, 32, 12, 4, 4, None, None) == _lib.SA_ERR_INVALID
+    assert lib.sa_memcpy_h2d(None, None, 0, None) == _lib.SA_OK  # zero bytes is a no-op
+    assert lib.sa_free(None) == _lib.SA_OK

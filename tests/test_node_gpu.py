@@ -1,0 +1,73 @@
+"""GPU parity of the Node.js binding: the JS shim runs the reference call forms on the device
+(tests/node/ops_gpu.js) and its outputs are checked against the CPU oracle (rel-L2 and normwise max
+relative error <= 1e-5)."""
+
+from __future__ import annotations
+
+import json
+import os
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+from oracle import attention as orc
+from supra_attn import workloads
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+NODE = shutil.which("node")
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(NODE is None, reason="node is not installed")]
+
+
+def _save(d, name, arr):
+    np.ascontiguousarray(arr).tofile(os.path.join(d, name))
+    return name
+
+
+def test_reference_call_forms_through_node(tmp_path):
+    d = str(tmp_path)
+    cases, refs = [], {}
+
+    s = workloads.dit_self(B=2, seed=10)
+    ref_s = orc.reference_torch(s).reshape(2 * 256, 576)
+    for form in ("dit_self_loop", "dit_self_batched"):
+        cases.append({"name": form, "form": form, "B": 2, "qkv": _save(d, "qkv.bin", s.q)})
+        refs[form] = ref_s
+
+    c = workloads.dit_cross(B=2, key_len=(77, 1), seed=11)
+    kv = c.k.reshape(2, 128, 1152)
+    cases.append({"name": "dit_cross_loop", "form": "dit_cross_loop", "B": 2, "L": [77, 1],
+                  "q": _save(d, "cq.bin", c.q),
+                  "kv": [_save(d, "kv0.bin", kv[0, :77]), _save(d, "kv1.bin", kv[1, :1])]})
+    refs["dit_cross_loop"] = orc.reference_torch(c).reshape(2 * 256, 576)
+
+    t5 = workloads.t5_self(seed=12, masked_tail=0)
+    t5_files = {"q": _save(d, "t5q.bin", t5.q), "k": _save(d, "t5k.bin", t5.k), "v": _save(d, "t5v.bin", t5.v),
+                "table": _save(d, "t5t.bin", t5.bias)}
+    cases.append(dict(name="t5_dense", form="t5_dense", L=128, **t5_files))
+    refs["t5_dense"] = orc.reference_torch(t5).reshape(128, 768)
+
+    t5m = workloads.t5_self(seed=12, masked_tail=40)
+    cases.append(dict(name="t5_relpos_mask", form="t5_relpos_mask", L=128, mask=_save(d, "t5m.bin", t5m.key_mask),
+                      **t5_files))
+    refs["t5_relpos_mask"] = orc.reference_torch(t5m).reshape(128, 768)
+
+    vae = workloads.vae_mid(seed=13)
+    cases.append({"name": "vae", "form": "vae", "L": 1024, "q": _save(d, "vq.bin", vae.q),
+                  "k": _save(d, "vk.bin", vae.k), "v": _save(d, "vv.bin", vae.v)})
+    refs["vae"] = orc.reference_torch(vae).reshape(1024, 512)
+
+    with open(os.path.join(d, "manifest.json"), "w") as f:
+        json.dump({"cases": cases}, f)
+    print("[node gpu] running", [c["name"] for c in cases], flush=True)
+    res = subprocess.run([NODE, os.path.join(ROOT, "tests", "node", "ops_gpu.js"), d], capture_output=True,
+                         text=True, timeout=300)
+    print(res.stdout, res.stderr, flush=True)
+    assert res.returncode == 0, res.stderr
+    for case in cases:
+        got = np.fromfile(os.path.join(d, case["name"] + ".out.bin"), dtype=np.float32)
+        ref = refs[case["name"]]
+        e = orc.errors(got.reshape(ref.shape), ref)
+        assert e["finite"] and e["rel_l2"] <= 1e-5 and e["max_rel"] <= 1e-5, f"{case['name']}: {e}"
