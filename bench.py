@@ -61,12 +61,13 @@ def time_calls(dev, launch, n: int, warmup: int) -> float:
     return e0.elapsed_ms(e1) / n
 
 
-def traffic_from_profiles(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summary, if any."""
+def traffic_from_profiles(workload: str):
+    """HBM bytes per launch of `workload`'s kernel from the committed rocprofv3 counter summary
+    (FETCH_SIZE and WRITE_SIZE passes scaled by a 256 MiB copy), if present."""
     path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
     try:
         with open(path) as f:
-            return json.load(f).get(kernel, {}).get("bytes_per_launch")
+            return json.load(f).get(workload, {}).get("bytes_per_launch")
     except (OSError, ValueError):
         return None
 
@@ -280,7 +281,7 @@ def main() -> int:
             "peak": PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_TFLOPS, 4),
-            "traffic": traffic_from_profiles(self_kernel),
+            "traffic": traffic_from_profiles("sweep_self"),
             "algorithmic_flops_per_launch": self_flops,
             "algorithmic_bytes_per_launch": self_call.algorithmic_bytes(),
             "us_per_launch": round(self_ms * 1e3, 3),
