@@ -13,7 +13,7 @@
 #include <stdlib.h>
 #include <string.h>
 
-#include "../../include/supra_attn.h"
+#include "supra_attn.h"
 #include "common.h"
 #include "kernels.h"
 

@@ -30,7 +30,9 @@
 //   output O / l, or 0 when every key is masked. The reference is moved (O and l rescaled by
 //   alpha = exp2(m_old - m_new)) only when some row's block maximum exceeds it by more than
 //   kRescaleSlack: otherwise p <= 2^kRescaleSlack and numerator and denominator share the same
-//   stale reference, so the quotient is unchanged while most blocks skip the rescale.
+//   stale reference, so the quotient is unchanged while most blocks skip the rescale. Every VALU
+//   instruction is issue time the SIMD's MFMA pipe loses (measured: ~4 cycles per VALU op,
+//   ~16 per exp), so the per-block VALU path is kept short.
 //
 // K/V tiles move HBM -> LDS with global_load_lds_dwordx4 (no VGPR staging), double-buffered: the
 // next tile streams in while the current one is consumed, one barrier per key block. Rows past the
@@ -64,8 +66,13 @@ __device__ __forceinline__ f32x16 zero16() {
   return z;
 }
 
+// Four workgroups (16 waves) per CU for the unbiased head-dim-64 single-split kernels, which fit
+// 128 VGPRs per wave without spilling (the bias and key-mask variants would spill).
 template <int D, int NSPLIT, int BIAS, int MASK>
-__global__ __launch_bounds__(256) void flash_mfma_kernel(AttnParams p, int q_tiles) {
+constexpr int kMinBlocksPerCU = (D == 64 && NSPLIT == 1 && BIAS == BIAS_NONE && MASK != MASK_KEY_MASK) ? 4 : 1;
+
+template <int D, int NSPLIT, int BIAS, int MASK>
+__global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void flash_mfma_kernel(AttnParams p, int q_tiles) {
   constexpr int QG = 4 / NSPLIT;         // query groups (of 32) per workgroup
   constexpr int QT = 32 * QG;            // queries per workgroup
   constexpr int KT = 32 * NSPLIT;        // keys staged per step
@@ -85,7 +92,8 @@ __global__ __launch_bounds__(256) void flash_mfma_kernel(AttnParams p, int q_til
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // wave-uniform in a scalar register, so per-block conditions compile to scalar branches
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qg = wave % QG;
   const int ks = wave / QG;
   const int col = lane & 31;
@@ -107,40 +115,51 @@ __global__ __launch_bounds__(256) void flash_mfma_kernel(AttnParams p, int q_til
   constexpr bool use_kmask = MASK == MASK_KEY_MASK;
   const uint8_t* kmask = use_kmask ? p.key_mask + (int64_t)b * p.smask : nullptr;
 
-  // ---- Q into registers, pre-scaled: lane holds scale*log2(e)*Q[qi][half*D/2 + s]
-  float qr[QREG];
-  {
-    const float* src = p.q + p.q_off + (int64_t)b * p.sq + (int64_t)qi * p.ldq + h * D + half * (D / 2);
-#pragma unroll
-    for (int i = 0; i < QREG / 4; ++i) {
-      f32x4 x = {0.f, 0.f, 0.f, 0.f};
-      if (q_valid) x = *reinterpret_cast<const f32x4*>(src + 4 * i);
-      qr[4 * i + 0] = x[0] * p.scale_log2;
-      qr[4 * i + 1] = x[1] * p.scale_log2;
-      qr[4 * i + 2] = x[2] * p.scale_log2;
-      qr[4 * i + 3] = x[3] * p.scale_log2;
-    }
-  }
-
   const float* kbase = p.k + p.k_off + (int64_t)b * p.sk + h * D;
   const float* vbase = p.v + p.v_off + (int64_t)b * p.sv + h * D;
 
-  // ---- issue the HBM -> LDS copy of step `step` into stage `buf`
+  // ---- HBM -> LDS copy of one step. Lane `lane` of instruction n fills physical chunk
+  // (n*4 + wave)*64 + lane of the tile: row `drow[n]`, logical chunk dck[n] (K) / dcv[n] (V).
+  // Full steps address rows from a wave-uniform base plus per-lane 32-bit offsets; the step
+  // holding the last valid key clamps rows past it to that key.
+  auto chunk_of = [&](int n, int& row, int& ck, int& cv) {
+    const int pc_all = (n * 4 + wave) * 64 + lane;
+    row = pc_all / CPR;
+    const int pc = pc_all % CPR;
+    ck = 4 * (pc ^ (row & 15));
+    cv = 4 * (pc ^ (((row >> 2) & 1) << 3));
+  };
+  unsigned koff[NI], voff[NI];  // byte offsets from the step's first row
+#pragma unroll
+  for (int n = 0; n < NI; ++n) {
+    int row, ck, cv;
+    chunk_of(n, row, ck, cv);
+    koff[n] = 4u * (unsigned)(row * (int)p.ldk + ck);
+    voff[n] = 4u * (unsigned)(row * (int)p.ldv + cv);
+  }
   auto issue = [&](int step, int buf) {
     float* kt = lds + buf * 2 * TILE;
     float* vt = kt + TILE;
     const int key0 = step * KT;
+    if (key0 + KT <= kv_len) {
+      const char* kb = reinterpret_cast<const char*>(kbase + (int64_t)key0 * p.ldk);
+      const char* vb = reinterpret_cast<const char*>(vbase + (int64_t)key0 * p.ldv);
 #pragma unroll
-    for (int n = 0; n < NI; ++n) {
-      const int blk64 = n * 4 + wave;        // 64-chunk (1 KiB) block of the tile
-      const int pc_all = blk64 * 64 + lane;  // physical chunk this lane fills
-      const int row = pc_all / CPR;
-      const int pc = pc_all % CPR;
-      const int key = min(key0 + row, kv_len - 1);
-      const int ck = pc ^ (row & 15);
-      const int cv = pc ^ (((row >> 2) & 1) << 3);
-      load_to_lds16(kbase + (int64_t)key * p.ldk + 4 * ck, kt + blk64 * 256);
-      load_to_lds16(vbase + (int64_t)key * p.ldv + 4 * cv, vt + blk64 * 256);
+      for (int n = 0; n < NI; ++n) {
+        const int blk64 = n * 4 + wave;  // 64-chunk (1 KiB) block of the tile
+        load_to_lds16(reinterpret_cast<const float*>(kb + koff[n]), kt + blk64 * 256);
+        load_to_lds16(reinterpret_cast<const float*>(vb + voff[n]), vt + blk64 * 256);
+      }
+    } else {
+#pragma unroll
+      for (int n = 0; n < NI; ++n) {
+        const int blk64 = n * 4 + wave;
+        int row, ck, cv;
+        chunk_of(n, row, ck, cv);
+        const int key = min(key0 + row, kv_len - 1);
+        load_to_lds16(kbase + (int64_t)key * p.ldk + ck, kt + blk64 * 256);
+        load_to_lds16(vbase + (int64_t)key * p.ldv + cv, vt + blk64 * 256);
+      }
     }
     if constexpr (BIAS == BIAS_RELPOS) {
       // entry e covers LUT index key0 - (q0 + QT - 1) + (Lq - 1) + e
@@ -171,7 +190,23 @@ __global__ __launch_bounds__(256) void flash_mfma_kernel(AttnParams p, int q_til
   float m = kMaxSeed;
   float l = 0.f;
 
-  if (nstep > 0) issue(0, 0);
+  if (nstep > 0) issue(0, 0);  // the first tile streams in while Q loads
+
+  // ---- Q into registers, pre-scaled: lane holds scale*log2(e)*Q[qi][half*D/2 + s]
+  float qr[QREG];
+  {
+    const float* src = p.q + p.q_off + (int64_t)b * p.sq + (int64_t)qi * p.ldq + h * D + half * (D / 2);
+#pragma unroll
+    for (int i = 0; i < QREG / 4; ++i) {
+      f32x4 x = {0.f, 0.f, 0.f, 0.f};
+      if (q_valid) x = *reinterpret_cast<const f32x4*>(src + 4 * i);
+      qr[4 * i + 0] = x[0] * p.scale_log2;
+      qr[4 * i + 1] = x[1] * p.scale_log2;
+      qr[4 * i + 2] = x[2] * p.scale_log2;
+      qr[4 * i + 3] = x[3] * p.scale_log2;
+    }
+  }
+
 
   for (int step = 0; step < nstep; ++step) {
     const int buf = step & 1;
@@ -244,10 +279,11 @@ __global__ __launch_bounds__(256) void flash_mfma_kernel(AttnParams p, int q_til
         for (int t = 0; t < NDB; ++t) oacc[t] *= alpha;
       }
       float ps = 0.f;
+      float pr[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        u[r] = fast_exp2(u[r] - m);
-        ps += u[r];
+        pr[r] = fast_exp2(u[r] - m);
+        ps += pr[r];
       }
       l += ps;
 
@@ -259,7 +295,7 @@ __global__ __launch_bounds__(256) void flash_mfma_kernel(AttnParams p, int q_til
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const float vv = vcol[(8 * (r >> 2) + (r & 3)) * D];
-          oacc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, u[r], oacc[t], 0, 0, 0);
+          oacc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, pr[r], oacc[t], 0, 0, 0);
         }
       }
     }
