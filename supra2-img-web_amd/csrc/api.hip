@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <math.h>
+#include <mutex>
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -148,13 +149,78 @@ int resolve(const sa_attn_args* a, sa::AttnParams* p) {
   return SA_OK;
 }
 
-enum class Path { kFlash, kGeneric };
+enum class Path { kFlash, kWide, kGeneric };
 
 struct Choice {
   Path path;
   int nsplit;
+  sa::WidePlan wide;
   const char* name;
 };
+
+// ---- per-device state: CU count and the wide kernel's workspace (grow-only, kept until exit)
+constexpr int kMaxDevices = 64;
+struct DeviceState {
+  int num_cus = 0;
+  float* ws = nullptr;
+  int64_t ws_floats = 0;
+  int* counters = nullptr;
+  int64_t n_counters = 0;
+};
+std::mutex g_dev_mutex;
+DeviceState g_dev[kMaxDevices];
+
+int current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return -1;
+  return dev;
+}
+
+// CU count of the current device (256 on MI355X); the MI355X value when no device is visible, so
+// that kernel selection can be inspected on a host without a GPU.
+int num_cus() {
+  const int dev = current_device();
+  if (dev < 0) return 256;
+  std::lock_guard<std::mutex> lock(g_dev_mutex);
+  DeviceState& st = g_dev[dev];
+  if (st.num_cus == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
+    st.num_cus = n;
+  }
+  return st.num_cus;
+}
+
+// Workspace of at least `floats` floats and `counters` zeroed int32 counters on the current
+// device. Allocated on first need and grown (never shrunk); the counters are zeroed on `stream`
+// when (re)allocated and every wide launch leaves them at zero.
+int wide_workspace(int64_t floats, int64_t counters, hipStream_t stream, float** ws, int** ctr) {
+  const int dev = current_device();
+  if (dev < 0) return fail(SA_ERR_HIP, "no current HIP device");
+  std::lock_guard<std::mutex> lock(g_dev_mutex);
+  DeviceState& st = g_dev[dev];
+  if (st.ws_floats < floats) {
+    if (st.ws) hipFree(st.ws);
+    st.ws = nullptr;
+    st.ws_floats = 0;
+    hipError_t e = hipMalloc(&st.ws, (size_t)floats * sizeof(float));
+    if (e != hipSuccess) return hip_fail(e, "workspace hipMalloc");
+    st.ws_floats = floats;
+  }
+  if (st.n_counters < counters) {
+    if (st.counters) hipFree(st.counters);
+    st.counters = nullptr;
+    st.n_counters = 0;
+    hipError_t e = hipMalloc(&st.counters, (size_t)counters * sizeof(int));
+    if (e != hipSuccess) return hip_fail(e, "workspace hipMalloc");
+    e = hipMemsetAsync(st.counters, 0, (size_t)counters * sizeof(int), stream);
+    if (e != hipSuccess) return hip_fail(e, "workspace hipMemsetAsync");
+    st.n_counters = counters;
+  }
+  *ws = st.ws;
+  *ctr = st.counters;
+  return SA_OK;
+}
 
 // Kernel selection. The MFMA kernels need D in {64, 128} and 16-byte aligned rows (the same gate
 // as the fused path of app/gpu/ops.js:111-112); everything else goes to the generic kernel.
@@ -176,6 +242,13 @@ int choose(const sa::AttnParams& p, Choice* c) {
     c->name = sa::flash_mfma_name(p.D, nsplit);
     return SA_OK;
   }
+  if (vec && sa::wide_mfma_supported(p)) {
+    c->path = Path::kWide;
+    c->nsplit = 1;
+    c->wide = sa::wide_mfma_plan(p, num_cus());
+    c->name = sa::wide_mfma_name(p.D);
+    return SA_OK;
+  }
   if (p.D > sa::GENERIC_MAX_D)
     return fail(SA_ERR_UNSUPPORTED, "head dim %d exceeds the supported maximum %d", p.D, sa::GENERIC_MAX_D);
   c->path = Path::kGeneric;
@@ -195,8 +268,20 @@ int sa_attention_f32(const sa_attn_args* args, void* stream) {
   Choice c;
   rc = choose(p, &c);
   if (rc != SA_OK) return rc;
-  hipError_t e = c.path == Path::kFlash ? sa::launch_flash_mfma(p, c.nsplit, (hipStream_t)stream)
-                                        : sa::launch_generic(p, (hipStream_t)stream);
+  hipError_t e;
+  if (c.path == Path::kFlash) {
+    e = sa::launch_flash_mfma(p, c.nsplit, (hipStream_t)stream);
+  } else if (c.path == Path::kWide) {
+    float* ws = nullptr;
+    int* counters = nullptr;
+    if (c.wide.nks > 1) {
+      rc = wide_workspace(c.wide.ws_floats, c.wide.counters, (hipStream_t)stream, &ws, &counters);
+      if (rc != SA_OK) return rc;
+    }
+    e = sa::launch_wide_mfma(p, c.wide, ws, counters, (hipStream_t)stream);
+  } else {
+    e = sa::launch_generic(p, (hipStream_t)stream);
+  }
   if (e != hipSuccess) return hip_fail(e, c.name);
   return ok();
 }

@@ -146,12 +146,42 @@ def test_relpos_matches_dense(dev):
 # ---- generic kernel (head dims / alignment outside the MFMA kernels)
 
 
-@pytest.mark.parametrize("D", [1, 32, 80, 512])
+@pytest.mark.parametrize("D", [1, 32, 80, 1000])
 def test_generic_head_dims(dev, D):
     call = make_call(B=2, H=2, D=D, Lq=33, Lk=300, seed=D)
     name = _lib.kernel_name(Staged(dev, call).args)
     assert name == "generic"
     run_checked(dev, call)
+
+
+# ---- wide-head kernel (D = 256 / 512: head dim split over waves, keys split over workgroups)
+
+
+@pytest.mark.parametrize("D,B,H,Lq,Lk", [(512, 1, 1, 1024, 1024), (512, 1, 1, 33, 300), (256, 2, 3, 70, 200),
+                                          (512, 2, 2, 64, 40), (256, 1, 1, 1, 1)])
+def test_wide_shapes(dev, D, B, H, Lq, Lk):
+    call = make_call(B=B, H=H, D=D, Lq=Lq, Lk=Lk, seed=D + Lq + Lk)
+    assert _lib.kernel_name(Staged(dev, call).args) == f"wide_mfma_d{D}"
+    run_checked(dev, call, check_fp64=Lq * Lk < 500000)
+
+
+def test_wide_key_len_and_repeat(dev):
+    """Key lengths (incl. 0 and ones that leave whole key chunks empty) and back-to-back calls that
+    reuse the merge counters."""
+    call = make_call(B=4, H=1, D=512, Lq=96, Lk=512, mask_mode=_lib.SA_MASK_KEY_LEN, key_len=[0, 1, 100, 512], seed=8)
+    st = Staged(dev, call)
+    assert st.kernel == "wide_mfma_d512"
+    ref = orc.reference_torch(call)
+    for _ in range(3):
+        out = st.run()
+        e = orc.errors(orc.output_view(out, call), ref)
+        assert e["finite"] and e["rel_l2"] <= TOL and e["max_rel"] <= TOL, e
+    st.release()
+
+
+def test_wide_large_batch_without_key_split(dev):
+    call = make_call(B=16, H=4, D=256, Lq=128, Lk=96, seed=12)
+    run_checked(dev, call, check_fp64=False)
 
 
 def test_generic_unaligned(dev):
