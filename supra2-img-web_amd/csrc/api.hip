@@ -164,8 +164,6 @@ struct DeviceState {
   int num_cus = 0;
   float* ws = nullptr;
   int64_t ws_floats = 0;
-  int* counters = nullptr;
-  int64_t n_counters = 0;
 };
 std::mutex g_dev_mutex;
 DeviceState g_dev[kMaxDevices];
@@ -191,34 +189,23 @@ int num_cus() {
   return st.num_cus;
 }
 
-// Workspace of at least `floats` floats and `counters` zeroed int32 counters on the current
-// device. Allocated on first need and grown (never shrunk); the counters are zeroed on `stream`
-// when (re)allocated and every wide launch leaves them at zero.
-int wide_workspace(int64_t floats, int64_t counters, hipStream_t stream, float** ws, int** ctr) {
+// Workspace of at least `floats` floats on the current device: allocated on first need and grown
+// (never shrunk), kept until the process exits. Calls that use it on one device are ordered by
+// their stream; concurrent calls on different streams of one device would share it and race.
+int wide_workspace(int64_t floats, float** ws) {
   const int dev = current_device();
   if (dev < 0) return fail(SA_ERR_HIP, "no current HIP device");
   std::lock_guard<std::mutex> lock(g_dev_mutex);
   DeviceState& st = g_dev[dev];
   if (st.ws_floats < floats) {
-    if (st.ws) hipFree(st.ws);
+    if (st.ws) (void)hipFree(st.ws);  // hipFree waits for kernels still reading the old one
     st.ws = nullptr;
     st.ws_floats = 0;
     hipError_t e = hipMalloc(&st.ws, (size_t)floats * sizeof(float));
     if (e != hipSuccess) return hip_fail(e, "workspace hipMalloc");
     st.ws_floats = floats;
   }
-  if (st.n_counters < counters) {
-    if (st.counters) hipFree(st.counters);
-    st.counters = nullptr;
-    st.n_counters = 0;
-    hipError_t e = hipMalloc(&st.counters, (size_t)counters * sizeof(int));
-    if (e != hipSuccess) return hip_fail(e, "workspace hipMalloc");
-    e = hipMemsetAsync(st.counters, 0, (size_t)counters * sizeof(int), stream);
-    if (e != hipSuccess) return hip_fail(e, "workspace hipMemsetAsync");
-    st.n_counters = counters;
-  }
   *ws = st.ws;
-  *ctr = st.counters;
   return SA_OK;
 }
 
@@ -273,12 +260,11 @@ int sa_attention_f32(const sa_attn_args* args, void* stream) {
     e = sa::launch_flash_mfma(p, c.nsplit, (hipStream_t)stream);
   } else if (c.path == Path::kWide) {
     float* ws = nullptr;
-    int* counters = nullptr;
     if (c.wide.nks > 1) {
-      rc = wide_workspace(c.wide.ws_floats, c.wide.counters, (hipStream_t)stream, &ws, &counters);
+      rc = wide_workspace(c.wide.ws_floats, &ws);
       if (rc != SA_OK) return rc;
     }
-    e = sa::launch_wide_mfma(p, c.wide, ws, counters, (hipStream_t)stream);
+    e = sa::launch_wide_mfma(p, c.wide, ws, (hipStream_t)stream);
   } else {
     e = sa::launch_generic(p, (hipStream_t)stream);
   }

@@ -37,19 +37,18 @@ hipError_t launch_flash_mfma(const AttnParams& p, int nsplit, hipStream_t stream
 const char* flash_mfma_name(int D, int nsplit);
 
 // Wide heads (D = 256 or 512, no bias, optional key lengths): head dim split across the waves of
-// a workgroup, keys split across workgroups with a merge through a workspace.
+// a workgroup, keys split across workgroups, partials merged by a second kernel via a workspace.
 constexpr int kWideMaxChunks = 16;
 struct WidePlan {
   int q_groups;       // 32-query groups per (sequence, head)
   int nks;            // key chunks per group (workgroups sharing one query group)
   int chunk;          // keys per chunk (multiple of 32)
   int64_t ws_floats;  // workspace floats (0 when nks == 1)
-  int64_t counters;   // int32 counters (one per query group, zero between calls)
 };
 bool wide_mfma_supported(const AttnParams& p);
 WidePlan wide_mfma_plan(const AttnParams& p, int num_cus);
 const char* wide_mfma_name(int D);
-hipError_t launch_wide_mfma(const AttnParams& p, const WidePlan& plan, float* ws, int* counters, hipStream_t stream);
+hipError_t launch_wide_mfma(const AttnParams& p, const WidePlan& plan, float* ws, hipStream_t stream);
 
 // Any head dim up to 1024, any alignment: one workgroup per query row.
 hipError_t launch_generic(const AttnParams& p, hipStream_t stream);

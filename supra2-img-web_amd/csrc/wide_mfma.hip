@@ -11,9 +11,9 @@
 //   slice. K and V slices are private to their wave: each wave streams its own slice into LDS
 //   with global_load_lds_dwordx4, and only the score exchange needs workgroup barriers.
 //   One head of 1024 queries gives just 32 query groups, so the keys are also split across
-//   workgroups (nks chunks). Each workgroup writes its partial (O, m, l) to a workspace; the last
-//   workgroup of a query group to finish (agent-scope atomic counter) merges the partials with
-//   the online-softmax rescale and writes the output, then resets the counter.
+//   workgroups (nks chunks). Each workgroup writes its partial (O, m, l) to a workspace and a
+//   second, fully parallel kernel merges the chunks of every query group with the online-softmax
+//   rescale (the kernel boundary orders the two; no atomics or cross-XCD fences).
 //
 // LDS per workgroup: K and V slices [32 keys][D/4] per wave (XOR-swizzled as in the flash kernel)
 // plus the score exchange: 144 KiB for D = 512 (one workgroup per CU), 80 KiB for D = 256.
@@ -51,8 +51,7 @@ __device__ __forceinline__ f32x16 zero16() {
 }
 
 template <int D, int MASK>
-__global__ __launch_bounds__(256, 1) void wide_mfma_kernel(AttnParams p, int q_groups, int nks, int chunk, float* ws,
-                                                           int* counters) {
+__global__ __launch_bounds__(256, 1) void wide_mfma_kernel(AttnParams p, int q_groups, int nks, int chunk, float* ws) {
   constexpr int DS = D / 4;       // head dims per wave
   constexpr int QREG = DS / 2;    // Q values per lane
   constexpr int NDB = DS / 32;    // 32-dim output tiles per wave
@@ -67,7 +66,6 @@ __global__ __launch_bounds__(256, 1) void wide_mfma_kernel(AttnParams p, int q_g
   __shared__ __attribute__((aligned(16))) float lds_k[4 * SLICE];  // [wave][SLICE]
   __shared__ __attribute__((aligned(16))) float lds_v[4 * SLICE];
   __shared__ __attribute__((aligned(16))) f32x4 lds_s[4 * 4 * 64];      // [wave][r/4][lane]
-  __shared__ int lds_last;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -257,89 +255,87 @@ __global__ __launch_bounds__(256, 1) void wide_mfma_kernel(AttnParams p, int q_g
     return;
   }
 
-  // ---- publish this chunk's partial: O (unnormalised, relative to m), m, l
+  // ---- publish this chunk's partial: O (unnormalised, relative to m), m, l; the merge kernel
+  // combines the chunks of each query group
   float* rec = ws + (int64_t)(slot_base + kc) * REC;
-  {
-    float* orow = rec + col * D + wave * DS + 4 * half;
+  float* orow = rec + col * D + wave * DS + 4 * half;
 #pragma unroll
-    for (int t = 0; t < NDB; ++t)
+  for (int t = 0; t < NDB; ++t)
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        f32x4 x;
-        x[0] = oacc[t][4 * g4 + 0];
-        x[1] = oacc[t][4 * g4 + 1];
-        x[2] = oacc[t][4 * g4 + 2];
-        x[3] = oacc[t][4 * g4 + 3];
-        *reinterpret_cast<f32x4*>(orow + 32 * t + 8 * g4) = x;
-      }
-    if (wave == 0 && half == 0) {
-      rec[32 * D + col] = m;
-      rec[32 * D + 32 + col] = lt;
+    for (int g4 = 0; g4 < 4; ++g4) {
+      f32x4 x;
+      x[0] = oacc[t][4 * g4 + 0];
+      x[1] = oacc[t][4 * g4 + 1];
+      x[2] = oacc[t][4 * g4 + 2];
+      x[3] = oacc[t][4 * g4 + 3];
+      *reinterpret_cast<f32x4*>(orow + 32 * t + 8 * g4) = x;
     }
+  if (wave == 0 && half == 0) {
+    rec[32 * D + col] = m;
+    rec[32 * D + 32 + col] = lt;
   }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const int done = __hip_atomic_fetch_add(counters + slot_base / nks, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    lds_last = done == nks - 1;
-  }
-  __syncthreads();
-  if (!lds_last) return;
-  __threadfence();
+}
 
-  // ---- last chunk of this query group: merge every partial with the online-softmax rescale
-  const float* recs = ws + (int64_t)slot_base * REC;
+// Combines the nks partial records of every query group: one thread per (query, 4 dims),
+// O = sum_c O_c exp2(m_c - m) / sum_c l_c exp2(m_c - m) with m = max_c m_c (0 if every l_c is 0).
+template <int D>
+__global__ __launch_bounds__(256) void wide_merge_kernel(AttnParams p, int q_groups, int nks, const float* ws) {
+  constexpr int REC = 32 * D + 64;
+  constexpr int C4 = D / 4;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)p.B * p.H * q_groups * 32 * C4;
+  if (idx >= total) return;
+  const int d4 = (int)(idx % C4);
+  int64_t r = idx / C4;
+  const int qq = (int)(r % 32);
+  r /= 32;  // (b*H + h)*q_groups + g
+  const int g = (int)(r % q_groups);
+  const int bh = (int)(r / q_groups);
+  const int h = bh % p.H;
+  const int b = bh / p.H;
+  const int qi = g * 32 + qq;
+  if (qi >= p.Lq) return;
+  const float* recs = ws + r * nks * REC;
   float mt = kMaxSeed;
-  for (int c = 0; c < nks; ++c) mt = fmaxf(mt, recs[(int64_t)c * REC + 32 * D + col]);
-  f32x16 acc[NDB];
-#pragma unroll
-  for (int t = 0; t < NDB; ++t) acc[t] = zero16();
+  for (int c = 0; c < nks; ++c) mt = fmaxf(mt, recs[(int64_t)c * REC + 32 * D + qq]);
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   float lsum = 0.f;
   for (int c = 0; c < nks; ++c) {
     const float* rc = recs + (int64_t)c * REC;
-    const float a = fast_exp2(rc[32 * D + col] - mt);
-    lsum = fmaf(rc[32 * D + 32 + col], a, lsum);
-    const float* orow = rc + col * D + wave * DS + 4 * half;
-#pragma unroll
-    for (int t = 0; t < NDB; ++t)
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const f32x4 x = *reinterpret_cast<const f32x4*>(orow + 32 * t + 8 * g4);
-        acc[t][4 * g4 + 0] = fmaf(x[0], a, acc[t][4 * g4 + 0]);
-        acc[t][4 * g4 + 1] = fmaf(x[1], a, acc[t][4 * g4 + 1]);
-        acc[t][4 * g4 + 2] = fmaf(x[2], a, acc[t][4 * g4 + 2]);
-        acc[t][4 * g4 + 3] = fmaf(x[3], a, acc[t][4 * g4 + 3]);
-      }
+    const float a = fast_exp2(rc[32 * D + qq] - mt);
+    lsum = fmaf(rc[32 * D + 32 + qq], a, lsum);
+    const f32x4 x = *reinterpret_cast<const f32x4*>(rc + qq * D + 4 * d4);
+    acc[0] = fmaf(x[0], a, acc[0]);
+    acc[1] = fmaf(x[1], a, acc[1]);
+    acc[2] = fmaf(x[2], a, acc[2]);
+    acc[3] = fmaf(x[3], a, acc[3]);
   }
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-  if (q_valid) {
-    float* dst = p.o + p.o_off + (int64_t)b * p.so + (int64_t)qi * p.ldo + h * D + wave * DS + 4 * half;
-#pragma unroll
-    for (int t = 0; t < NDB; ++t)
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        f32x4 x;
-        x[0] = acc[t][4 * g4 + 0] * inv;
-        x[1] = acc[t][4 * g4 + 1] * inv;
-        x[2] = acc[t][4 * g4 + 2] * inv;
-        x[3] = acc[t][4 * g4 + 3] * inv;
-        *reinterpret_cast<f32x4*>(dst + 32 * t + 8 * g4) = x;
-      }
-  }
-  if (tid == 0) __hip_atomic_store(counters + slot_base / nks, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  f32x4 y;
+  y[0] = acc[0] * inv;
+  y[1] = acc[1] * inv;
+  y[2] = acc[2] * inv;
+  y[3] = acc[3] * inv;
+  *reinterpret_cast<f32x4*>(p.o + p.o_off + (int64_t)b * p.so + (int64_t)qi * p.ldo + h * D + 4 * d4) = y;
 }
 
 template <int D>
-hipError_t launch_d(const AttnParams& p, const WidePlan& plan, float* ws, int* counters, hipStream_t stream) {
+hipError_t launch_d(const AttnParams& p, const WidePlan& plan, float* ws, hipStream_t stream) {
   const int64_t n = (int64_t)p.B * p.H * plan.q_groups * plan.nks;
   if (n > 0x7fffffff) return hipErrorInvalidConfiguration;
   const dim3 grid((unsigned)n), block(256);
   if (p.mask_mode == MASK_KEY_LEN)
     hipLaunchKernelGGL((wide_mfma_kernel<D, MASK_KEY_LEN>), grid, block, 0, stream, p, plan.q_groups, plan.nks,
-                       plan.chunk, ws, counters);
+                       plan.chunk, ws);
   else
     hipLaunchKernelGGL((wide_mfma_kernel<D, MASK_NONE>), grid, block, 0, stream, p, plan.q_groups, plan.nks,
-                       plan.chunk, ws, counters);
+                       plan.chunk, ws);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || plan.nks == 1) return e;
+  const int64_t threads = (int64_t)p.B * p.H * plan.q_groups * 32 * (D / 4);
+  const int64_t blocks = (threads + 255) / 256;
+  if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL((wide_merge_kernel<D>), dim3((unsigned)blocks), block, 0, stream, p, plan.q_groups, plan.nks, ws);
   return hipGetLastError();
 }
 
@@ -364,15 +360,14 @@ WidePlan wide_mfma_plan(const AttnParams& p, int num_cus) {
   plan.chunk = 32 * blocks_per_chunk;
   plan.nks = (p.Lk + plan.chunk - 1) / plan.chunk;  // chunks that hold at least one key
   plan.ws_floats = plan.nks > 1 ? base * plan.nks * (int64_t)(32 * p.D + 64) : 0;
-  plan.counters = plan.nks > 1 ? base : 0;
   return plan;
 }
 
 const char* wide_mfma_name(int D) { return D == 512 ? "wide_mfma_d512" : "wide_mfma_d256"; }
 
-hipError_t launch_wide_mfma(const AttnParams& p, const WidePlan& plan, float* ws, int* counters, hipStream_t stream) {
-  if (p.D == 512) return launch_d<512>(p, plan, ws, counters, stream);
-  if (p.D == 256) return launch_d<256>(p, plan, ws, counters, stream);
+hipError_t launch_wide_mfma(const AttnParams& p, const WidePlan& plan, float* ws, hipStream_t stream) {
+  if (p.D == 512) return launch_d<512>(p, plan, ws, stream);
+  if (p.D == 256) return launch_d<256>(p, plan, ws, stream);
   return hipErrorInvalidValue;
 }
 
