@@ -287,14 +287,16 @@ __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void
       }
       l += ps;
 
-      // ---- O^T += V^T P^T; V element (row, 32t + col) sits in chunk (8t + col/4) ^ 8*half
+      // ---- O^T += V^T P^T; V element (row, 32t + col) sits in chunk (8t + col/4) ^ 8*half.
+      // The D/32 output tiles are independent accumulation chains: interleaving them (each P
+      // register feeding one MFMA per tile in turn) keeps the MFMA pipe fed while an exp2 or an
+      // LDS read is still in flight.
       const float* vrow = vt + (ks * 32 + 4 * half) * D + col;
 #pragma unroll
-      for (int t = 0; t < NDB; ++t) {
-        const float* vcol = vrow + 32 * (t ^ half);
+      for (int r = 0; r < 16; ++r) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float vv = vcol[(8 * (r >> 2) + (r & 3)) * D];
+        for (int t = 0; t < NDB; ++t) {
+          const float vv = vrow[32 * (t ^ half) + (8 * (r >> 2) + (r & 3)) * D];
           oacc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, pr[r], oacc[t], 0, 0, 0);
         }
       }
