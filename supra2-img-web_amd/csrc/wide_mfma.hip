@@ -296,19 +296,39 @@ __global__ __launch_bounds__(256) void wide_merge_kernel(AttnParams p, int q_gro
   const int qi = g * 32 + qq;
   if (qi >= p.Lq) return;
   const float* recs = ws + r * nks * REC;
+  // Chunks go in groups of 4 whose loads are all issued before any is used (indexes clamped to
+  // the last chunk, surplus lanes of a group masked out), so a query costs ceil(nks/4) load round
+  // trips per pass instead of nks.
   float mt = kMaxSeed;
-  for (int c = 0; c < nks; ++c) mt = fmaxf(mt, recs[(int64_t)c * REC + 32 * D + qq]);
+  for (int c0 = 0; c0 < nks; c0 += 4) {
+    float mv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) mv[u] = recs[(int64_t)min(c0 + u, nks - 1) * REC + 32 * D + qq];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) mt = fmaxf(mt, mv[u]);  // a repeated last chunk changes nothing
+  }
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   float lsum = 0.f;
-  for (int c = 0; c < nks; ++c) {
-    const float* rc = recs + (int64_t)c * REC;
-    const float a = fast_exp2(rc[32 * D + qq] - mt);
-    lsum = fmaf(rc[32 * D + 32 + qq], a, lsum);
-    const f32x4 x = *reinterpret_cast<const f32x4*>(rc + qq * D + 4 * d4);
-    acc[0] = fmaf(x[0], a, acc[0]);
-    acc[1] = fmaf(x[1], a, acc[1]);
-    acc[2] = fmaf(x[2], a, acc[2]);
-    acc[3] = fmaf(x[3], a, acc[3]);
+  for (int c0 = 0; c0 < nks; c0 += 4) {
+    float mv[4], lv[4];
+    f32x4 xv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float* rc = recs + (int64_t)min(c0 + u, nks - 1) * REC;
+      mv[u] = rc[32 * D + qq];
+      lv[u] = rc[32 * D + 32 + qq];
+      xv[u] = *reinterpret_cast<const f32x4*>(rc + qq * D + 4 * d4);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (c0 + u >= nks) break;
+      const float a = fast_exp2(mv[u] - mt);
+      lsum = fmaf(lv[u], a, lsum);
+      acc[0] = fmaf(xv[u][0], a, acc[0]);
+      acc[1] = fmaf(xv[u][1], a, acc[1]);
+      acc[2] = fmaf(xv[u][2], a, acc[2]);
+      acc[3] = fmaf(xv[u][3], a, acc[3]);
+    }
   }
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
   f32x4 y;
