@@ -224,14 +224,34 @@ __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void
       f32x16 s = zero16();
       const float* krow = kt + (ks * 32 + col) * D;
       const int ksw = col & 15;
+      // Key-split variants (head dim 64) run one or two waves per SIMD with registers to spare: all
+      // K operands of the block are read before the MFMA chain, so it never waits on LDS (with 4
+      // waves per SIMD the other waves hide those waits and the registers are not there).
+      constexpr bool kPrefetch = NSPLIT > 1 && D == 64;
+      f32x4 kpre[kPrefetch ? QREG / 4 : 1];
+      if constexpr (kPrefetch) {
+#pragma unroll
+        for (int i = 0; i < QREG / 4; ++i)
+          kpre[i] = *reinterpret_cast<const f32x4*>(krow + 4 * ((half * (CPR / 2) + i) ^ ksw));
+      }
 #pragma unroll
       for (int i = 0; i < QREG / 4; ++i) {
         const int c = (half * (CPR / 2) + i) ^ ksw;
-        const f32x4 kv = *reinterpret_cast<const f32x4*>(krow + 4 * c);
+        const f32x4 kv = kPrefetch ? kpre[i] : *reinterpret_cast<const f32x4*>(krow + 4 * c);
         s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[0], qr[4 * i + 0], s, 0, 0, 0);
         s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[1], qr[4 * i + 1], s, 0, 0, 0);
         s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[2], qr[4 * i + 2], s, 0, 0, 0);
         s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[3], qr[4 * i + 3], s, 0, 0, 0);
+      }
+      // likewise the V operands of the PV step (head dim 64), read while the softmax runs
+      constexpr bool vPrefetch = NSPLIT > 1 && D == 64;
+      const float* vrow = vt + (ks * 32 + 4 * half) * D + col;
+      float vpre[vPrefetch ? 16 * NDB : 1];
+      if constexpr (vPrefetch) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+#pragma unroll
+          for (int t = 0; t < NDB; ++t) vpre[r * NDB + t] = vrow[32 * (t ^ half) + (8 * (r >> 2) + (r & 3)) * D];
       }
 
       // ---- bias and masks
@@ -291,12 +311,11 @@ __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void
       // The D/32 output tiles are independent accumulation chains: interleaving them (each P
       // register feeding one MFMA per tile in turn) keeps the MFMA pipe fed while an exp2 or an
       // LDS read is still in flight.
-      const float* vrow = vt + (ks * 32 + 4 * half) * D + col;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
 #pragma unroll
         for (int t = 0; t < NDB; ++t) {
-          const float vv = vrow[32 * (t ^ half) + (8 * (r >> 2) + (r & 3)) * D];
+          const float vv = vPrefetch ? vpre[r * NDB + t] : vrow[32 * (t ^ half) + (8 * (r >> 2) + (r & 3)) * D];
           oacc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, pr[r], oacc[t], 0, 0, 0);
         }
       }
