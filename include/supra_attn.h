@@ -14,7 +14,8 @@
  *  - Offsets and strides are in ELEMENTS (floats for q/k/v/o/bias), as in app/gpu/ops.js.
  *  - All calls are stream-ordered and asynchronous unless documented otherwise; `stream` is a
  *    hipStream_t passed as void* (NULL = the null stream). Nothing in the attention call
- *    allocates device memory.
+ *    allocates device memory: the kernels that merge partial results across workgroups use a
+ *    caller-provided workspace (sa_attention_workspace_bytes).
  *  - Status codes: SA_OK (0) or a negative SA_ERR_* value. A failed call launches nothing.
  *    sa_last_error() returns a thread-local message describing the last failure.
  *  - q, k and v may alias one another (the DiT passes one packed qkv buffer as all three,
@@ -30,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SA_ABI_VERSION 1
+#define SA_ABI_VERSION 2
 
 /* ---- status codes ---- */
 #define SA_OK 0
@@ -96,12 +97,22 @@ typedef struct sa_attn_args {
   const int32_t* key_len;             /* KEY_LEN: [B] */
   const uint8_t* key_mask;            /* KEY_MASK: [B, smask] */
   int64_t smask;                      /* KEY_MASK batch stride (bytes = elements); <= 0 means Lk */
+  void* workspace;                    /* device scratch, 16-byte aligned, when the call needs it */
+  int64_t workspace_bytes;            /* its size (>= sa_attention_workspace_bytes(args)) */
 } sa_attn_args;
 
 /* Fused attention, fp32 in and out, fp32 MFMA arithmetic. Replaces ops.attention
  * (app/gpu/ops.js:103-149) for every caller in app/models/{dit,t5,vae}.js; B folds the
  * per-sample host loops of app/models/dit.js:170-185 into one launch. Asynchronous on `stream`. */
 int sa_attention_f32(const sa_attn_args* args, void* stream);
+
+/* Device scratch bytes sa_attention_f32 needs for these arguments on the current device (0 for
+ * most calls; the wide-head kernel splits long key ranges across workgroups and merges their
+ * partial results through it), or a negative SA_ERR_* status if the arguments are rejected.
+ * The workspace holds no state between calls, but calls that run concurrently must not share one.
+ * Host only: no device work. There is no counterpart in the reference, whose unfused path keeps
+ * its score matrix in buffers the caller's pool provides (app/gpu/ops.js:125-128). */
+int64_t sa_attention_workspace_bytes(const sa_attn_args* args);
 
 /* Which kernel sa_attention_f32 would launch for these arguments (a static name such as
  * "flash_mfma_d64"), or NULL with sa_last_error() set if the arguments are rejected. Host only. */

@@ -158,12 +158,10 @@ struct Choice {
   const char* name;
 };
 
-// ---- per-device state: CU count and the wide kernel's workspace (grow-only, kept until exit)
+// ---- per-device state: CU count
 constexpr int kMaxDevices = 64;
 struct DeviceState {
   int num_cus = 0;
-  float* ws = nullptr;
-  int64_t ws_floats = 0;
 };
 std::mutex g_dev_mutex;
 DeviceState g_dev[kMaxDevices];
@@ -187,26 +185,6 @@ int num_cus() {
     st.num_cus = n;
   }
   return st.num_cus;
-}
-
-// Workspace of at least `floats` floats on the current device: allocated on first need and grown
-// (never shrunk), kept until the process exits. Calls that use it on one device are ordered by
-// their stream; concurrent calls on different streams of one device would share it and race.
-int wide_workspace(int64_t floats, float** ws) {
-  const int dev = current_device();
-  if (dev < 0) return fail(SA_ERR_HIP, "no current HIP device");
-  std::lock_guard<std::mutex> lock(g_dev_mutex);
-  DeviceState& st = g_dev[dev];
-  if (st.ws_floats < floats) {
-    if (st.ws) (void)hipFree(st.ws);  // hipFree waits for kernels still reading the old one
-    st.ws = nullptr;
-    st.ws_floats = 0;
-    hipError_t e = hipMalloc(&st.ws, (size_t)floats * sizeof(float));
-    if (e != hipSuccess) return hip_fail(e, "workspace hipMalloc");
-    st.ws_floats = floats;
-  }
-  *ws = st.ws;
-  return SA_OK;
 }
 
 // Kernel selection. The MFMA kernels need D in {64, 128} and 16-byte aligned rows (the same gate
@@ -260,9 +238,20 @@ int sa_attention_f32(const sa_attn_args* args, void* stream) {
     e = sa::launch_flash_mfma(p, c.nsplit, (hipStream_t)stream);
   } else if (c.path == Path::kWide) {
     float* ws = nullptr;
-    if (c.wide.nks > 1) {
-      rc = wide_workspace(c.wide.ws_floats, &ws);
-      if (rc != SA_OK) return rc;
+    if (c.wide.ws_floats > 0) {
+      const int64_t need = c.wide.ws_floats * (int64_t)sizeof(float);
+      if (!args->workspace || args->workspace_bytes < need)
+        return fail(SA_ERR_INVALID, "this call needs a device workspace of %lld bytes (sa_attention_workspace_bytes)",
+                    (long long)need);
+      if (!aligned16(args->workspace)) return fail(SA_ERR_INVALID, "workspace must be 16-byte aligned");
+      const Extent ew = {(uintptr_t)args->workspace, (uintptr_t)args->workspace + (uintptr_t)need};
+      const int64_t HD = (int64_t)p.H * p.D;
+      if (overlaps(ew, extent(p.o, p.o_off, p.so, p.ldo, p.B, p.Lq, HD)) ||
+          overlaps(ew, extent(p.q, p.q_off, p.sq, p.ldq, p.B, p.Lq, HD)) ||
+          overlaps(ew, extent(p.k, p.k_off, p.sk, p.ldk, p.B, p.Lk, HD)) ||
+          overlaps(ew, extent(p.v, p.v_off, p.sv, p.ldv, p.B, p.Lk, HD)))
+        return fail(SA_ERR_ALIAS, "the workspace overlaps q, k, v or o");
+      ws = static_cast<float*>(args->workspace);
     }
     e = sa::launch_wide_mfma(p, c.wide, ws, (hipStream_t)stream);
   } else {
@@ -270,6 +259,17 @@ int sa_attention_f32(const sa_attn_args* args, void* stream) {
   }
   if (e != hipSuccess) return hip_fail(e, c.name);
   return ok();
+}
+
+int64_t sa_attention_workspace_bytes(const sa_attn_args* args) {
+  sa::AttnParams p;
+  int rc = resolve(args, &p);
+  if (rc != SA_OK) return rc;
+  Choice c;
+  rc = choose(p, &c);
+  if (rc != SA_OK) return rc;
+  ok();
+  return c.path == Path::kWide ? c.wide.ws_floats * (int64_t)sizeof(float) : 0;
 }
 
 const char* sa_attention_kernel_name(const sa_attn_args* args) {

@@ -153,12 +153,13 @@ static int prop_ptr(napi_env env, napi_value obj, const char* name, void** out) 
 
 /* opts -> sa_attn_args. Field names are those of app/gpu/ops.js:109 (q, k, v, Lq, Lk, H, D, ldq,
  * ldk, ldv, qOff, kOff, vOff, oOff, scale) plus out -> o, and the extension fields B, ldo, sq, sk,
- * sv, so, biasMode, bias, sbias, bucketLut, numBuckets, maskMode, keyLen, keyMask, smask. */
+ * sv, so, biasMode, bias, sbias, bucketLut, numBuckets, maskMode, keyLen, keyMask, smask,
+ * workspace, workspaceBytes. */
 static int fill_args(napi_env env, napi_value o, sa_attn_args* a) {
   memset(a, 0, sizeof *a);
   a->struct_size = sizeof *a;
   int64_t B, H, D, Lq, Lk, bm, mm, nb;
-  void *q, *k, *v, *out, *bias, *lut, *kl, *km;
+  void *q, *k, *v, *out, *bias, *lut, *kl, *km, *ws;
   double scale;
   napi_value sv;
   if (prop_i64(env, o, "B", 1, &B) || prop_i64(env, o, "H", -1, &H) || prop_i64(env, o, "D", -1, &D) ||
@@ -166,7 +167,7 @@ static int fill_args(napi_env env, napi_value o, sa_attn_args* a) {
     return 1;
   if (prop_ptr(env, o, "q", &q) || prop_ptr(env, o, "k", &k) || prop_ptr(env, o, "v", &v) ||
       prop_ptr(env, o, "out", &out) || prop_ptr(env, o, "bias", &bias) || prop_ptr(env, o, "bucketLut", &lut) ||
-      prop_ptr(env, o, "keyLen", &kl) || prop_ptr(env, o, "keyMask", &km))
+      prop_ptr(env, o, "keyLen", &kl) || prop_ptr(env, o, "keyMask", &km) || prop_ptr(env, o, "workspace", &ws))
     return 1;
   if (prop_i64(env, o, "qOff", 0, &a->q_off) || prop_i64(env, o, "kOff", 0, &a->k_off) ||
       prop_i64(env, o, "vOff", 0, &a->v_off) || prop_i64(env, o, "oOff", 0, &a->o_off) ||
@@ -175,7 +176,8 @@ static int fill_args(napi_env env, napi_value o, sa_attn_args* a) {
       prop_i64(env, o, "sq", 0, &a->sq) || prop_i64(env, o, "sk", 0, &a->sk) || prop_i64(env, o, "sv", 0, &a->sv) ||
       prop_i64(env, o, "so", 0, &a->so) || prop_i64(env, o, "sbias", 0, &a->sbias) ||
       prop_i64(env, o, "smask", 0, &a->smask) || prop_i64(env, o, "biasMode", SA_BIAS_NONE, &bm) ||
-      prop_i64(env, o, "maskMode", SA_MASK_NONE, &mm) || prop_i64(env, o, "numBuckets", 0, &nb))
+      prop_i64(env, o, "maskMode", SA_MASK_NONE, &mm) || prop_i64(env, o, "numBuckets", 0, &nb) ||
+      prop_i64(env, o, "workspaceBytes", 0, &a->workspace_bytes))
     return 1;
   if (prop(env, o, "scale", &sv) || get_f64(env, sv, 1.0, &scale, "scale")) return 1;
   if (B < -0x7fffffffLL || B > 0x7fffffffLL || H > 0x7fffffffLL || D > 0x7fffffffLL || Lq > 0x7fffffffLL ||
@@ -200,6 +202,7 @@ static int fill_args(napi_env env, napi_value o, sa_attn_args* a) {
   a->mask_mode = (int32_t)mm;
   a->key_len = (const int32_t*)kl;
   a->key_mask = (const uint8_t*)km;
+  a->workspace = ws;
   return 0;
 }
 
@@ -216,6 +219,22 @@ static napi_value js_attention(napi_env env, napi_callback_info info) {
   if (ensure_stream(env)) return NULL;
   if (throw_if(env, sa_attention_f32(&a, g_stream))) return NULL;
   return undefined(env);
+}
+
+/* Bytes of device workspace the call needs (sa_attention_workspace_bytes); throws if rejected. */
+static napi_value js_workspace_bytes(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (get_args(env, info, 1, argv)) return NULL;
+  sa_attn_args a;
+  if (fill_args(env, argv[0], &a)) return NULL;
+  const int64_t n = sa_attention_workspace_bytes(&a);
+  if (n < 0) {
+    throw_if(env, (int)n);
+    return NULL;
+  }
+  napi_value r;
+  NAPI_CALL(env, napi_create_double(env, (double)n, &r));
+  return r;
 }
 
 static napi_value js_kernel_name(napi_env env, napi_callback_info info) {
@@ -452,6 +471,7 @@ static napi_value init(napi_env env, napi_value exports) {
   const napi_property_descriptor props[] = {
       {"attention", NULL, js_attention, NULL, NULL, NULL, napi_enumerable, NULL},
       {"kernelName", NULL, js_kernel_name, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"workspaceBytes", NULL, js_workspace_bytes, NULL, NULL, NULL, napi_enumerable, NULL},
       {"version", NULL, js_version, NULL, NULL, NULL, napi_enumerable, NULL},
       {"deviceCount", NULL, js_device_count, NULL, NULL, NULL, napi_enumerable, NULL},
       {"malloc", NULL, js_malloc, NULL, NULL, NULL, napi_enumerable, NULL},

@@ -88,7 +88,21 @@ function nativeArgs(o, out) {
 function attention(gpu, o) {
   var B = def(o.B, 1);
   var out = o.out || gpu.empty([B * o.Lq, o.H * o.D]);
-  gpu.native.attention(nativeArgs(o, out));
+  var args = nativeArgs(o, out);
+  // device scratch for the calls that merge partial results across workgroups (wide heads), from
+  // the pool and released right away: the pool hands buffers out again in queue order
+  var wsBytes = gpu.native.workspaceBytes(args);
+  var ws = null;
+  if (wsBytes > 0) {
+    ws = gpu.empty([Math.ceil(wsBytes / 4)]);
+    args.workspace = ws.buf;
+    args.workspaceBytes = wsBytes;
+  }
+  try {
+    gpu.native.attention(args);
+  } finally {
+    if (ws) ws.release();
+  }
   return out;
 }
 

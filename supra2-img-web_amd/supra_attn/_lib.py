@@ -31,6 +31,7 @@ SA_MASK_KEY_MASK = 2
 SIGNATURES = {
     "sa_attention_f32": (c_int, [c_void_p, c_void_p]),
     "sa_attention_kernel_name": (c_char_p, [c_void_p]),
+    "sa_attention_workspace_bytes": (c_int64, [c_void_p]),
     "sa_t5_bucket_lut": (c_int, [c_int32, c_int32, c_int32, c_int32, c_int32, POINTER(c_int32)]),
     "sa_t5_position_bias": (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p]),
     "sa_device_count": (c_int, [POINTER(c_int32)]),
@@ -99,6 +100,8 @@ class AttnArgs(ctypes.Structure):
         ("key_len", c_void_p),
         ("key_mask", c_void_p),
         ("smask", c_int64),
+        ("workspace", c_void_p),
+        ("workspace_bytes", c_int64),
     ]
 
     def __init__(self, **kw):
@@ -143,6 +146,15 @@ def kernel_name(args: AttnArgs) -> str:
     if name is None:
         raise SaError(-1, lib.sa_last_error().decode())
     return name.decode()
+
+
+def workspace_bytes(args: AttnArgs) -> int:
+    """Device scratch bytes sa_attention_f32 needs for `args` (0 for most calls)."""
+    lib = load()
+    n = lib.sa_attention_workspace_bytes(ctypes.byref(args))
+    if n < 0:
+        raise SaError(int(n), lib.sa_last_error().decode())
+    return int(n)
 
 
 def bucket_lut(Lq: int, Lk: int, num_buckets: int = 32, max_distance: int = 128, bidirectional: bool = True):

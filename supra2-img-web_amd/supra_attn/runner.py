@@ -39,6 +39,12 @@ class Staged:
             kw["key_mask"] = self._put(km).ptr
             kw.setdefault("smask", km.shape[-1])
         self.args = _lib.AttnArgs(**kw)
+        ws_bytes = _lib.workspace_bytes(self.args)
+        if ws_bytes > 0:  # scratch for the calls that merge partial results (wide heads)
+            ws = dev.empty(((ws_bytes + 3) // 4,))
+            self.bufs.append(ws)
+            self.args.workspace = ws.ptr
+            self.args.workspace_bytes = ws_bytes
 
     def _put(self, arr):
         buf = self.dev.from_array(np.ascontiguousarray(arr))

@@ -22,11 +22,11 @@ function check(name, fn) {
 }
 
 check("addon exports", function () {
-  ["attention", "kernelName", "version", "deviceCount", "malloc", "free", "upload", "download", "memset", "sync",
+  ["attention", "kernelName", "workspaceBytes", "version", "deviceCount", "malloc", "free", "upload", "download", "memset", "sync",
     "bucketLut", "positionBias", "eventCreate", "eventRecord", "eventElapsed", "eventDestroy"].forEach(function (f) {
     assert.strictEqual(typeof native[f], "function", f);
   });
-  assert.strictEqual(native.version(), 1);
+  assert.strictEqual(native.version(), 2);
   assert.strictEqual(native.SA_BIAS_RELPOS, 2);
   assert.strictEqual(native.SA_MASK_KEY_MASK, 2);
 });
@@ -67,12 +67,15 @@ function fakeNative() {
     mallocs: 0,
     deviceCount: function () { return 1; },
     malloc: function (bytes) { this.mallocs++; return { id: ++n, bytes: bytes }; },
-    free: function () {},
+    free: function () { this.frees++; },
     upload: function () {},
     download: function () {},
     sync: function () {},
     attention: function (a) { this.calls.push(a); },
     kernelName: function () { return "fake"; },
+    wsBytes: 0,
+    frees: 0,
+    workspaceBytes: function () { return this.wsBytes; },
     bucketLut: native.bucketLut,
   };
 }
@@ -164,6 +167,24 @@ check("VAE form (vae.js:86): one head, D = 512, default scale", function () {
   assert.strictEqual(a.scale, 1 / Math.sqrt(512));
   assert.strictEqual(a.ldo, 512);
   assert.strictEqual(a.so, 512 * 1024);
+  assert.strictEqual(a.workspace, undefined);
+  // a call that needs device scratch gets a pooled buffer, returned to the pool after the launch
+  g.f.wsBytes = 16805888;
+  sa.attention(g.gpu, { q: q, k: q, v: q, Lq: 1024, Lk: 1024, H: 1, D: 512, ldq: 512, ldk: 512, ldv: 512 });
+  var w = g.f.calls[1];
+  assert.strictEqual(w.workspaceBytes, 16805888);
+  assert.ok(w.workspace && w.workspace.bytes >= 16805888);
+  var before = g.f.mallocs;
+  var again = g.gpu.empty([16805888 / 4]);
+  assert.strictEqual(again.buf, w.workspace);
+  assert.strictEqual(g.f.mallocs, before);
+  // the workspace goes back to the pool when the launch throws, too
+  g.f.attention = function () { throw new Error("launch failed"); };
+  again.release();
+  assert.throws(function () {
+    sa.attention(g.gpu, { q: q, k: q, v: q, Lq: 1024, Lk: 1024, H: 1, D: 512, ldq: 512, ldk: 512, ldv: 512 });
+  }, /launch failed/);
+  assert.strictEqual(g.gpu.empty([16805888 / 4]).buf, w.workspace);
 });
 
 check("released tensors are reused and cannot be passed again", function () {

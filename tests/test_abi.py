@@ -39,7 +39,7 @@ def test_every_declared_symbol_is_exported_and_bound():
 
 def test_version_and_constants():
     lib = _lib.load()
-    assert lib.sa_version() == 1
+    assert lib.sa_version() == 2
     text = open(HEADER).read()
     for name in ("SA_OK", "SA_ERR_INVALID", "SA_ERR_UNSUPPORTED", "SA_ERR_HIP", "SA_ERR_ALIAS", "SA_BIAS_NONE",
                  "SA_BIAS_DENSE", "SA_BIAS_RELPOS", "SA_MASK_NONE", "SA_MASK_KEY_LEN", "SA_MASK_KEY_MASK"):
@@ -172,3 +172,37 @@ def test_device_helpers_reject_null_pointers():
     assert lib.sa_t5_position_bias(None, None, 32, 12, 4, 4, None, None) == _lib.SA_ERR_INVALID
     assert lib.sa_memcpy_h2d(None, None, 0, None) == _lib.SA_OK  # zero bytes is a no-op
     assert lib.sa_free(None) == _lib.SA_OK
+
+
+def vae_args(**over):
+    kw = dict(B=1, H=1, D=512, Lq=1024, Lk=1024, q=FAKE, k=FAKE + (1 << 24), v=FAKE + (2 << 24), o=FAKE + (3 << 24),
+              ldq=512, ldk=512, ldv=512, scale=0.0442)
+    kw.update(over)
+    return _lib.AttnArgs(**kw)
+
+
+def test_workspace_size_query():
+    # flash and generic kernels need none; the wide-head kernel needs one partial record per key chunk
+    assert _lib.workspace_bytes(good_args()) == 0
+    assert _lib.workspace_bytes(good_args(D=32, ldo=288, so=256 * 288)) == 0
+    need = _lib.workspace_bytes(vae_args())
+    assert need > 0 and need % 16 == 0
+    assert need < 64 << 20
+    with pytest.raises(_lib.SaError) as e:
+        _lib.workspace_bytes(good_args(B=0))
+    assert e.value.code == _lib.SA_ERR_INVALID
+
+
+@pytest.mark.parametrize("over,code,text", [
+    (dict(), _lib.SA_ERR_INVALID, "workspace of"),
+    (dict(workspace=FAKE + (8 << 24)), _lib.SA_ERR_INVALID, "workspace of"),
+    (dict(workspace=FAKE + (8 << 24), workspace_bytes="need-1"), _lib.SA_ERR_INVALID, "workspace of"),
+    (dict(workspace=FAKE + (8 << 24) + 4, workspace_bytes="need"), _lib.SA_ERR_INVALID, "aligned"),
+    (dict(workspace=FAKE + (3 << 24) - 64, workspace_bytes="need"), _lib.SA_ERR_ALIAS, "overlaps"),
+    (dict(workspace=FAKE + (1 << 24) + 4096, workspace_bytes="need"), _lib.SA_ERR_ALIAS, "overlaps"),
+])
+def test_workspace_is_checked_before_launch(over, code, text):
+    need = _lib.workspace_bytes(vae_args())
+    over = {k: (need - 1 if v == "need-1" else need if v == "need" else v) for k, v in over.items()}
+    assert rc_of(vae_args(**over)) == code
+    assert text in _lib.load().sa_last_error().decode()

@@ -165,17 +165,30 @@ def test_wide_shapes(dev, D, B, H, Lq, Lk):
     run_checked(dev, call, check_fp64=Lq * Lk < 500000)
 
 
-def test_wide_key_len_and_repeat(dev):
-    """Key lengths (incl. 0 and ones that leave whole key chunks empty) and back-to-back calls that
-    reuse the merge counters."""
+def test_wide_key_len_and_workspace_reuse(dev):
+    """Key lengths (incl. 0 and ones that leave whole key chunks empty); back-to-back calls on one
+    workspace that is refilled with NaN bytes before each call (no result may depend on what the
+    workspace held), then a smaller call on the same, larger workspace."""
     call = make_call(B=4, H=1, D=512, Lq=96, Lk=512, mask_mode=_lib.SA_MASK_KEY_LEN, key_len=[0, 1, 100, 512], seed=8)
     st = Staged(dev, call)
     assert st.kernel == "wide_mfma_d512"
+    ws = st.bufs[-1]
+    assert st.args.workspace == ws.ptr and ws.nbytes >= st.args.workspace_bytes > 0
     ref = orc.reference_torch(call)
     for _ in range(3):
+        ws.fill_bytes(0xFF)
         out = st.run()
         e = orc.errors(orc.output_view(out, call), ref)
         assert e["finite"] and e["rel_l2"] <= TOL and e["max_rel"] <= TOL, e
+    small = make_call(B=1, H=1, D=512, Lq=33, Lk=300, seed=9)
+    s2 = Staged(dev, small)
+    assert 0 < _lib.workspace_bytes(s2.args) <= ws.nbytes
+    s2.args.workspace = ws.ptr
+    s2.args.workspace_bytes = ws.nbytes
+    ws.fill_bytes(0xFF)
+    e = orc.errors(orc.output_view(s2.run(), small), orc.reference_torch(small))
+    assert e["finite"] and e["rel_l2"] <= TOL and e["max_rel"] <= TOL, e
+    s2.release()
     st.release()
 
 
