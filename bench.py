@@ -12,7 +12,7 @@ The same JSON line carries:
   roofline     the dominant kernel (sweep self-attention), timed per launch with HIP events
   cpu_baseline the PyTorch fp32 CPU formulation of tools/reference.py:72-79 on a bounded sample
 
-    python bench.py [--steps 50] [--warmup 3] [--cpu-steps 4] [--no-cpu]
+    python bench.py [--steps 50] [--warmup 3] [--cpu-seconds 12] [--no-cpu]
 
 `--profile WORKLOAD` instead launches one workload (sweep_self, sweep_cross or a single-call
 config) `--launches` times, then copies a 256 MiB device buffer 4 times with the runtime's copy
@@ -72,9 +72,9 @@ def traffic_from_profiles(workload: str):
         return None
 
 
-def cpu_baseline(data, steps: int) -> dict:
-    """PyTorch fp32 CPU on `steps` full sweep steps (28 calls each), the tools/reference.py
-    formulation, inputs already in host memory."""
+def cpu_baseline(data, seconds: float) -> dict:
+    """PyTorch fp32 CPU on whole sweep steps (28 calls each), the tools/reference.py formulation,
+    inputs already in host memory, repeated until `seconds` of CPU work have been timed."""
     import torch
 
     from oracle import attention as orc
@@ -85,11 +85,18 @@ def cpu_baseline(data, steps: int) -> dict:
     # warm-up call
     orc.cpu_dit_self(blocks[0][0])
     t0 = time.perf_counter()
-    for st in range(steps):
+    steps, last = 0, t0
+    while True:
         for s, c in blocks:
             orc.cpu_dit_self(s)
             orc.cpu_dit_cross(c)
-        log(f"cpu baseline step {st + 1}/{steps} done")
+        steps += 1
+        now = time.perf_counter()
+        if now - t0 >= seconds:
+            break
+        if now - last >= 5.0:
+            log(f"cpu baseline: {steps} steps in {now - t0:.1f} s")
+            last = now
     dt = time.perf_counter() - t0
     return {
         "value": flops * steps / dt / 1e12,
@@ -140,7 +147,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--cpu-steps", type=int, default=4)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calls", type=int, default=200, help="calls per single-config timing")
     ap.add_argument("--profile", default=None, help="launch only this workload (for rocprofv3 counter passes)")
@@ -239,8 +246,8 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu:
-        log(f"cpu baseline: {args.cpu_steps} steps")
-        cpu = cpu_baseline(data, args.cpu_steps)
+        log(f"cpu baseline: whole sweep steps for {args.cpu_seconds:g} s")
+        cpu = cpu_baseline(data, args.cpu_seconds)
         log(f"cpu baseline: {cpu['value']:.4f} TFLOP/s")
 
     head = per_config["dit_self_b2"]
