@@ -12,7 +12,7 @@ The same JSON line carries:
   roofline     the dominant kernel (sweep self-attention), timed per launch with HIP events
   cpu_baseline the PyTorch fp32 CPU formulation of tools/reference.py:72-79 on a bounded sample
 
-    python bench.py [--steps 50] [--warmup 3] [--cpu-seconds 12] [--no-cpu]
+    python bench.py [--steps 50] [--warmup 20] [--cpu-seconds 12] [--no-cpu]
 
 `--profile WORKLOAD` instead launches one workload (sweep_self, sweep_cross or a single-call
 config) `--launches` times, then copies a 256 MiB device buffer 4 times with the runtime's copy
@@ -146,7 +146,7 @@ def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=20)  # ~40 ms: the clocks settle after ~25 ms of load
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calls", type=int, default=200, help="calls per single-config timing")

@@ -235,7 +235,7 @@ int sa_attention_f32(const sa_attn_args* args, void* stream) {
   if (rc != SA_OK) return rc;
   hipError_t e;
   if (c.path == Path::kFlash) {
-    e = sa::launch_flash_mfma(p, c.nsplit, (hipStream_t)stream);
+    e = sa::launch_flash_mfma(p, c.nsplit, num_cus(), (hipStream_t)stream);
   } else if (c.path == Path::kWide) {
     float* ws = nullptr;
     if (c.wide.ws_floats > 0) {

@@ -14,7 +14,9 @@
 //
 // Per 32-key block a wave computes the transposed score tile S^T = K Q^T with 32x32x2 fp32 MFMAs:
 //   A operand  K[key = lane%32][d], B operand Q^T[d][query = lane%32], the head dim split between
-//   the two half-waves (d = half*D/2 + s, s = 0..D/2-1). Q stays in VGPRs for the whole kernel.
+//   the two half-waves by 16-byte chunks: half-wave `half` takes chunks 2i + half (i = 0..D/8-1),
+//   so each Q load instruction reads 32 contiguous bytes per row. Q stays in VGPRs for the whole
+//   kernel.
 //   Accumulator layout: lane l holds query l%32 and keys 8*(r/4) + 4*(l/32) + r%4 in register r,
 //   so the row max and row sum of a query are in-lane over 16 registers plus one exchange with
 //   lane l^32 (v_permlane32_swap).
@@ -37,6 +39,16 @@
 // K/V tiles move HBM -> LDS with global_load_lds_dwordx4 (no VGPR staging), double-buffered: the
 // next tile streams in while the current one is consumed, one barrier per key block. Rows past the
 // last valid key re-read the last valid row (finite data, masked out of the softmax).
+//
+// Start-up and output (single-split kernels):
+//   - At launch every resident workgroup asks for its Q rows and first K/V tile at once (48 KiB
+//     each, ~48 MB over a full chip at 4 workgroups per CU); served interleaved, the median
+//     workgroup waited ~11 us for its first tile while the MFMA pipes idled. The g-th workgroup of
+//     each CU of the first residency (dispatch order: blockIdx / num_cus) therefore starts its loads
+//     g * kStaggerTicks later, so the memory system serves one workgroup per CU first and compute
+//     starts within a few microseconds while the rest streams in.
+//   - O is staged through LDS (the K/V tiles are free by then) and written as whole 256-byte rows
+//     instead of 32-byte pieces of 32 rows per instruction, which the memory system absorbs faster.
 // LDS tiles are [KT keys][D] in 16-byte chunks, XOR-swizzled per row:
 //   K: chunk c of row r at c ^ (r & 15), so the b128 reads of 16 consecutive rows hit all banks;
 //   V: chunk c of row r at c ^ (8 * ((r >> 2) & 1)), so the two half-waves (rows 4 apart) read
@@ -71,8 +83,12 @@ __device__ __forceinline__ f32x16 zero16() {
 template <int D, int NSPLIT, int BIAS, int MASK>
 constexpr int kMinBlocksPerCU = (D == 64 && NSPLIT == 1 && BIAS == BIAS_NONE && MASK != MASK_KEY_MASK) ? 4 : 1;
 
+// Start-up stagger step, in ticks of the 100 MHz real-time counter (3.5 us): about the time the
+// memory system takes to deliver the first tiles of one workgroup per CU over the whole chip.
+constexpr unsigned kStaggerTicks = 350;
+
 template <int D, int NSPLIT, int BIAS, int MASK>
-__global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void flash_mfma_kernel(AttnParams p, int q_tiles) {
+__global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void flash_mfma_kernel(AttnParams p, int q_tiles, int stagger_cus) {
   constexpr int QG = 4 / NSPLIT;         // query groups (of 32) per workgroup
   constexpr int QT = 32 * QG;            // queries per workgroup
   constexpr int KT = 32 * NSPLIT;        // keys staged per step
@@ -190,16 +206,27 @@ __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void
   float m = kMaxSeed;
   float l = 0.f;
 
+  // ---- start-up stagger (stagger_cus > 0 only for the 4-workgroups-per-CU kernels): the g-th
+  // workgroup of each CU in the first residency waits g steps before its first loads
+  if constexpr (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK> == 4) {
+    if (stagger_cus > 0) {
+      const unsigned gen = blockIdx.x / (unsigned)stagger_cus;
+      if (gen > 0 && gen < 4) {
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        while (__builtin_amdgcn_s_memrealtime() - t0 < gen * kStaggerTicks) __builtin_amdgcn_s_sleep(2);
+      }
+    }
+  }
   if (nstep > 0) issue(0, 0);  // the first tile streams in while Q loads
 
-  // ---- Q into registers, pre-scaled: lane holds scale*log2(e)*Q[qi][half*D/2 + s]
+  // ---- Q into registers, pre-scaled: lane holds scale*log2(e)*Q[qi][8i + 4*half + j] in qr[4i + j]
   float qr[QREG];
   {
-    const float* src = p.q + p.q_off + (int64_t)b * p.sq + (int64_t)qi * p.ldq + h * D + half * (D / 2);
+    const float* src = p.q + p.q_off + (int64_t)b * p.sq + (int64_t)qi * p.ldq + h * D;
 #pragma unroll
     for (int i = 0; i < QREG / 4; ++i) {
       f32x4 x = {0.f, 0.f, 0.f, 0.f};
-      if (q_valid) x = *reinterpret_cast<const f32x4*>(src + 4 * i);
+      if (q_valid) x = *reinterpret_cast<const f32x4*>(src + 4 * (2 * i + half));
       qr[4 * i + 0] = x[0] * p.scale_log2;
       qr[4 * i + 1] = x[1] * p.scale_log2;
       qr[4 * i + 2] = x[2] * p.scale_log2;
@@ -232,11 +259,11 @@ __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void
       if constexpr (kPrefetch) {
 #pragma unroll
         for (int i = 0; i < QREG / 4; ++i)
-          kpre[i] = *reinterpret_cast<const f32x4*>(krow + 4 * ((half * (CPR / 2) + i) ^ ksw));
+          kpre[i] = *reinterpret_cast<const f32x4*>(krow + 4 * ((2 * i + half) ^ ksw));
       }
 #pragma unroll
       for (int i = 0; i < QREG / 4; ++i) {
-        const int c = (half * (CPR / 2) + i) ^ ksw;
+        const int c = (2 * i + half) ^ ksw;
         const f32x4 kv = kPrefetch ? kpre[i] : *reinterpret_cast<const f32x4*>(krow + 4 * c);
         s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[0], qr[4 * i + 0], s, 0, 0, 0);
         s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[1], qr[4 * i + 1], s, 0, 0, 0);
@@ -361,7 +388,35 @@ __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void
   // ---- normalise and store: lane holds O[qi][32t + 8g + 4*half + 0..3] in registers 4g..4g+3
   const float lt = sum_with_partner(l);
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
-  if (q_valid) {
+  if constexpr (NSPLIT == 1) {
+    // through LDS: each wave writes its 32 x D tile (16-byte chunks swizzled by row, conflict-free
+    // both ways) and reads it back as whole rows, CPR lanes per row
+    __syncthreads();  // every wave is done with the K/V tiles
+    float* ot = lds + wave * 32 * D;
+#pragma unroll
+    for (int t = 0; t < NDB; ++t) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        f32x4 x;
+        x[0] = oacc[t][4 * g + 0] * inv;
+        x[1] = oacc[t][4 * g + 1] * inv;
+        x[2] = oacc[t][4 * g + 2] * inv;
+        x[3] = oacc[t][4 * g + 3] * inv;
+        const int c = (8 * t + 2 * g + half) ^ (col & 15);
+        *reinterpret_cast<f32x4*>(ot + col * D + 4 * c) = x;
+      }
+    }
+    constexpr int RPI = 64 / CPR;  // rows per store instruction
+    const int rsub = lane / CPR, cidx = lane % CPR;
+    float* obase = p.o + p.o_off + (int64_t)b * p.so + h * D + 4 * cidx;
+#pragma unroll
+    for (int j = 0; j < 32 / RPI; ++j) {
+      const int row = RPI * j + rsub;
+      const f32x4 x = *reinterpret_cast<const f32x4*>(ot + row * D + 4 * (cidx ^ (row & 15)));
+      const int qrow = q0 + qg * 32 + row;
+      if (qrow < p.Lq) *reinterpret_cast<f32x4*>(obase + (int64_t)qrow * p.ldo) = x;
+    }
+  } else if (q_valid) {
     float* dst = p.o + p.o_off + (int64_t)b * p.so + (int64_t)qi * p.ldo + h * D + 4 * half;
 #pragma unroll
     for (int t = 0; t < NDB; ++t) {
@@ -379,32 +434,34 @@ __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void
 }
 
 template <int D, int NSPLIT, int BIAS, int MASK>
-hipError_t launch_one(const AttnParams& p, int q_tiles, dim3 grid, hipStream_t stream) {
-  hipLaunchKernelGGL((flash_mfma_kernel<D, NSPLIT, BIAS, MASK>), grid, dim3(256), 0, stream, p, q_tiles);
+hipError_t launch_one(const AttnParams& p, int q_tiles, dim3 grid, int num_cus, hipStream_t stream) {
+  // stagger only launches with more than one workgroup per CU
+  const int stagger_cus = (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK> == 4 && (int64_t)grid.x > num_cus) ? num_cus : 0;
+  hipLaunchKernelGGL((flash_mfma_kernel<D, NSPLIT, BIAS, MASK>), grid, dim3(256), 0, stream, p, q_tiles, stagger_cus);
   return hipGetLastError();
 }
 
 template <int D, int NSPLIT, int BIAS>
-hipError_t launch_mask(const AttnParams& p, int q_tiles, dim3 grid, hipStream_t stream) {
+hipError_t launch_mask(const AttnParams& p, int q_tiles, dim3 grid, int num_cus, hipStream_t stream) {
   switch (p.mask_mode) {
-    case MASK_NONE: return launch_one<D, NSPLIT, BIAS, MASK_NONE>(p, q_tiles, grid, stream);
-    case MASK_KEY_LEN: return launch_one<D, NSPLIT, BIAS, MASK_KEY_LEN>(p, q_tiles, grid, stream);
-    case MASK_KEY_MASK: return launch_one<D, NSPLIT, BIAS, MASK_KEY_MASK>(p, q_tiles, grid, stream);
+    case MASK_NONE: return launch_one<D, NSPLIT, BIAS, MASK_NONE>(p, q_tiles, grid, num_cus, stream);
+    case MASK_KEY_LEN: return launch_one<D, NSPLIT, BIAS, MASK_KEY_LEN>(p, q_tiles, grid, num_cus, stream);
+    case MASK_KEY_MASK: return launch_one<D, NSPLIT, BIAS, MASK_KEY_MASK>(p, q_tiles, grid, num_cus, stream);
     default: return hipErrorInvalidValue;
   }
 }
 
 template <int D, int NSPLIT>
-hipError_t launch_split(const AttnParams& p, hipStream_t stream) {
+hipError_t launch_split(const AttnParams& p, int num_cus, hipStream_t stream) {
   constexpr int QT = 32 * (4 / NSPLIT);
   const int q_tiles = (p.Lq + QT - 1) / QT;
   const int64_t n = (int64_t)p.B * p.H * q_tiles;
   if (n > 0x7fffffff) return hipErrorInvalidConfiguration;
   const dim3 grid((unsigned)n);
   switch (p.bias_mode) {
-    case BIAS_NONE: return launch_mask<D, NSPLIT, BIAS_NONE>(p, q_tiles, grid, stream);
-    case BIAS_DENSE: return launch_mask<D, NSPLIT, BIAS_DENSE>(p, q_tiles, grid, stream);
-    case BIAS_RELPOS: return launch_mask<D, NSPLIT, BIAS_RELPOS>(p, q_tiles, grid, stream);
+    case BIAS_NONE: return launch_mask<D, NSPLIT, BIAS_NONE>(p, q_tiles, grid, num_cus, stream);
+    case BIAS_DENSE: return launch_mask<D, NSPLIT, BIAS_DENSE>(p, q_tiles, grid, num_cus, stream);
+    case BIAS_RELPOS: return launch_mask<D, NSPLIT, BIAS_RELPOS>(p, q_tiles, grid, num_cus, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -417,15 +474,15 @@ const char* flash_mfma_name(int D, int nsplit) {
   return nullptr;
 }
 
-hipError_t launch_flash_mfma(const AttnParams& p, int nsplit, hipStream_t stream) {
+hipError_t launch_flash_mfma(const AttnParams& p, int nsplit, int num_cus, hipStream_t stream) {
   if (p.D == 64) {
-    if (nsplit == 4) return launch_split<64, 4>(p, stream);
-    if (nsplit == 2) return launch_split<64, 2>(p, stream);
-    return launch_split<64, 1>(p, stream);
+    if (nsplit == 4) return launch_split<64, 4>(p, num_cus, stream);
+    if (nsplit == 2) return launch_split<64, 2>(p, num_cus, stream);
+    return launch_split<64, 1>(p, num_cus, stream);
   }
   if (p.D == 128) {
-    if (nsplit >= 2) return launch_split<128, 2>(p, stream);
-    return launch_split<128, 1>(p, stream);
+    if (nsplit >= 2) return launch_split<128, 2>(p, num_cus, stream);
+    return launch_split<128, 1>(p, num_cus, stream);
   }
   return hipErrorInvalidValue;
 }

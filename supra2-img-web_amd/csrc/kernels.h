@@ -32,8 +32,9 @@ enum { BIAS_NONE = 0, BIAS_DENSE = 1, BIAS_RELPOS = 2 };
 enum { MASK_NONE = 0, MASK_KEY_LEN = 1, MASK_KEY_MASK = 2 };
 
 // Flash kernel on fp32 MFMA for D in {64, 128} with 16-byte aligned rows.
-// nsplit in {1, 2, 4}: key blocks are split across the 4 waves of a workgroup.
-hipError_t launch_flash_mfma(const AttnParams& p, int nsplit, hipStream_t stream);
+// nsplit in {1, 2, 4}: key blocks are split across the 4 waves of a workgroup. num_cus (the
+// device's CU count) sets the start-up stagger of the single-split kernels.
+hipError_t launch_flash_mfma(const AttnParams& p, int nsplit, int num_cus, hipStream_t stream);
 const char* flash_mfma_name(int D, int nsplit);
 
 // Wide heads (D = 256 or 512, no bias, optional key lengths): head dim split across the waves of
