@@ -111,6 +111,48 @@ def cpu_baseline(data, seconds: float) -> dict:
     }
 
 
+def callsite_block(dev, s_st, c_st, reps: int = 20) -> dict:
+    """One DiT block's attention at batch B issued as app/models/dit.js:169-185 issues it (one launch
+    per sample: B self-attention calls on the packed qkv, then B cross-attention calls at each
+    sample's true key length) against the two batched launches, on the same device-resident inputs."""
+    import ctypes
+
+    from supra_attn import _lib
+    from supra_attn.device import Event
+
+    sa, ca = s_st.args, c_st.args
+    B = sa.B
+    key_len = c_st.call.key_len
+    per = []
+    for a, lens in ((sa, None), (ca, key_len)):
+        for b in range(B):
+            per.append(_lib.AttnArgs(
+                B=1, H=a.H, D=a.D, Lq=a.Lq, Lk=a.Lk if lens is None else int(lens[b]), q=a.q, k=a.k, v=a.v, o=a.o,
+                q_off=a.q_off + b * a.sq, k_off=a.k_off + b * a.sk, v_off=a.v_off + b * a.sv, o_off=a.o_off + b * a.so,
+                ldq=a.ldq, ldk=a.ldk, ldv=a.ldv, ldo=a.ldo, scale=a.scale))
+    lib = _lib.load()
+    stream = ctypes.c_void_p(dev.stream)
+    refs = [ctypes.byref(a) for a in per]
+
+    def loop():
+        for r in refs:
+            rc = lib.sa_attention_f32(r, stream)
+            if rc:
+                _lib.check(rc)
+
+    def batched():
+        s_st.launch()
+        c_st.launch()
+
+    out = {"workload": f"one DiT block's attention at batch {B}: self + cross (sweep block 0)"}
+    for name, fn, n in (("per_sample", loop, len(per)), ("batched", batched, 2)):
+        ms = time_calls(dev, fn, reps, warmup=3)
+        out[f"{name}_us"] = round(ms * 1e3, 2)
+        out[f"{name}_launches"] = n
+    out["speedup"] = round(out["per_sample_us"] / out["batched_us"], 2)
+    return out
+
+
 COPY_BYTES = 256 << 20
 
 
@@ -222,6 +264,11 @@ def main() -> int:
     cross_flops = sum(c.call.flops() for _, c in staged) / len(staged)
     log(f"per launch: self {self_ms * 1e3:.1f} us ({achieved:.1f} TFLOP/s), cross {cross_ms * 1e3:.1f} us")
 
+    # caller side: per-sample launches (the reference's loops) against the batched call sites
+    callsite = callsite_block(dev, staged[0][0], staged[0][1])
+    log(f"call sites, one block: per-sample {callsite['per_sample_us']:.1f} us ({callsite['per_sample_launches']} "
+        f"launches) vs batched {callsite['batched_us']:.1f} us (2 launches): {callsite['speedup']:.2f}x")
+
     # single-call configs
     per_config = {}
     for name, make in workloads.CONFIGS.items():
@@ -297,6 +344,7 @@ def main() -> int:
         },
         "per_config": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                        for k, v in per_config.items()},
+        "callsite": callsite,
         "cpu_baseline": None if cpu is None else {k: (round(v, 6) if isinstance(v, float) else v) for k, v in cpu.items()},
     }
     print(json.dumps(result))

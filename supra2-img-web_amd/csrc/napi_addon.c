@@ -375,6 +375,26 @@ static napi_value js_memset(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
+/* (dst, dstByteOffset, src, srcByteOffset, bytes): device-to-device copy, stream-ordered */
+static napi_value js_copy(napi_env env, napi_callback_info info) {
+  napi_value argv[5];
+  if (get_args(env, info, 5, argv)) return NULL;
+  void* dst;
+  void* src;
+  int64_t doff, soff, bytes;
+  if (get_ptr(env, argv[0], &dst, "dst") || get_i64(env, argv[1], 0, &doff, "dstByteOffset") ||
+      get_ptr(env, argv[2], &src, "src") || get_i64(env, argv[3], 0, &soff, "srcByteOffset") ||
+      get_i64(env, argv[4], -1, &bytes, "bytes"))
+    return NULL;
+  if (!dst || !src || doff < 0 || soff < 0 || bytes < 0) {
+    napi_throw_error(env, "SA_ERR_INVALID", "copy needs two buffers and offsets, bytes >= 0");
+    return NULL;
+  }
+  if (ensure_stream(env)) return NULL;
+  if (throw_if(env, sa_memcpy_d2d((char*)dst + doff, (const char*)src + soff, (size_t)bytes, g_stream))) return NULL;
+  return undefined(env);
+}
+
 static napi_value js_sync(napi_env env, napi_callback_info info) {
   (void)info;
   if (ensure_stream(env)) return NULL;
@@ -479,6 +499,7 @@ static napi_value init(napi_env env, napi_value exports) {
       {"upload", NULL, js_upload, NULL, NULL, NULL, napi_enumerable, NULL},
       {"download", NULL, js_download, NULL, NULL, NULL, napi_enumerable, NULL},
       {"memset", NULL, js_memset, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"copy", NULL, js_copy, NULL, NULL, NULL, napi_enumerable, NULL},
       {"sync", NULL, js_sync, NULL, NULL, NULL, napi_enumerable, NULL},
       {"bucketLut", NULL, js_bucket_lut, NULL, NULL, NULL, napi_enumerable, NULL},
       {"positionBias", NULL, js_position_bias, NULL, NULL, NULL, napi_enumerable, NULL},

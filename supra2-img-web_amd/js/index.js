@@ -1,8 +1,10 @@
-// Entry point of the JS binding: the device runtime and the attention operator.
+// Entry point of the JS binding: the device runtime, the attention operator and the batched DiT
+// call sites.
 "use strict";
 
 var device = require("./device");
 var ops = require("./ops");
+var dit = require("./dit_attn");
 
 module.exports = {
   GPU: device.GPU,
@@ -13,4 +15,5 @@ module.exports = {
   relativeBucket: ops.relativeBucket,
   relposBias: ops.relposBias,
   positionBias: ops.positionBias,
+  dit: dit,
 };

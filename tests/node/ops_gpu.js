@@ -59,6 +59,24 @@ var forms = {
     q.release();
     return out;
   },
+  // the batched call-site helpers (js/dit_attn.js): one launch each for the whole batch
+  dit_self_callsite: function (gpu, c) {
+    var qkv = gpu.fromArray(loadBin(c.qkv), [c.B * 256, 3 * 576]);
+    var a = sa.dit.selfAttention(gpu, qkv, c.B);
+    qkv.release();
+    return a;
+  },
+  dit_cross_callsite: function (gpu, c) {
+    var q = gpu.fromArray(loadBin(c.q), [c.B * 256, 576]);
+    var kvs = [];
+    for (var b = 0; b < c.B; b++) kvs.push(gpu.fromArray(loadBin(c.kv[b]), [c.L[b], 2 * 576]));
+    var ctx = sa.dit.packContexts(gpu, kvs, c.L);
+    kvs.forEach(function (t) { t.release(); });
+    var out = sa.dit.crossAttention(gpu, q, ctx);
+    ctx.release();
+    q.release();
+    return out;
+  },
   // app/models/t5.js:73-80: dense [H, L, L] position bias, scale 1 (bias built on the device)
   t5_dense: function (gpu, c) {
     var q = gpu.fromArray(loadBin(c.q), [c.L, 768]);

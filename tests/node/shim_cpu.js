@@ -22,7 +22,7 @@ function check(name, fn) {
 }
 
 check("addon exports", function () {
-  ["attention", "kernelName", "workspaceBytes", "version", "deviceCount", "malloc", "free", "upload", "download", "memset", "sync",
+  ["attention", "kernelName", "workspaceBytes", "version", "deviceCount", "malloc", "free", "upload", "download", "memset", "copy", "sync",
     "bucketLut", "positionBias", "eventCreate", "eventRecord", "eventElapsed", "eventDestroy"].forEach(function (f) {
     assert.strictEqual(typeof native[f], "function", f);
   });
@@ -69,6 +69,8 @@ function fakeNative() {
     malloc: function (bytes) { this.mallocs++; return { id: ++n, bytes: bytes }; },
     free: function () { this.frees++; },
     upload: function () {},
+    copies: [],
+    copy: function (dst, doff, src, soff, bytes) { this.copies.push([dst, doff, src, soff, bytes]); },
     download: function () {},
     sync: function () {},
     attention: function (a) { this.calls.push(a); },
@@ -185,6 +187,42 @@ check("VAE form (vae.js:86): one head, D = 512, default scale", function () {
     sa.attention(g.gpu, { q: q, k: q, v: q, Lq: 1024, Lk: 1024, H: 1, D: 512, ldq: 512, ldk: 512, ldv: 512 });
   }, /launch failed/);
   assert.strictEqual(g.gpu.empty([16805888 / 4]).buf, w.workspace);
+});
+
+check("batched DiT call sites: one launch per block (dit.js:169-173, 180-185)", function () {
+  var g = makeGpu();
+  var D = 576, TOK = 256, B = 4;
+  var qkv = g.gpu.empty([B * TOK, 3 * D]);
+  var a = sa.dit.selfAttention(g.gpu, qkv, B);
+  assert.strictEqual(g.f.calls.length, 1);
+  var s = g.f.calls[0];
+  assert.strictEqual(s.B, B);
+  assert.strictEqual(s.q, qkv.buf);
+  assert.strictEqual(s.kOff, D);
+  assert.strictEqual(s.vOff, 2 * D);
+  assert.strictEqual(s.sq, TOK * 3 * D);
+  assert.strictEqual(s.so, TOK * D);
+  assert.deepStrictEqual(a.shape, [B * TOK, D]);
+  var lens = [77, 1, 50, 0];
+  var kvs = lens.map(function (L) { return g.gpu.empty([Math.max(L, 1), 2 * D]); });
+  var ctx = sa.dit.packContexts(g.gpu, kvs, lens);
+  assert.strictEqual(ctx.Lmax, 77);
+  assert.strictEqual(g.f.copies.length, 3);  // the empty context copies nothing
+  assert.deepStrictEqual(g.f.copies[1], [ctx.kv.buf, 1 * 77 * 2 * D * 4, kvs[1].buf, 0, 1 * 2 * D * 4]);
+  assert.deepStrictEqual(g.f.copies[2], [ctx.kv.buf, 2 * 77 * 2 * D * 4, kvs[2].buf, 0, 50 * 2 * D * 4]);
+  var q = g.gpu.empty([B * TOK, D]);
+  sa.dit.crossAttention(g.gpu, q, ctx);
+  assert.strictEqual(g.f.calls.length, 2);
+  var c = g.f.calls[1];
+  assert.strictEqual(c.B, B);
+  assert.strictEqual(c.Lk, 77);
+  assert.strictEqual(c.keyLen, ctx.keyLen.buf);
+  assert.strictEqual(c.vOff, D);
+  assert.strictEqual(c.sk, 77 * 2 * D);
+  assert.strictEqual(c.ldk, 2 * D);
+  ctx.release();
+  assert.strictEqual(ctx.kv.buf, null);
+  assert.throws(function () { sa.dit.packContexts(g.gpu, kvs, [1, 2]); }, RangeError);
 });
 
 check("released tensors are reused and cannot be passed again", function () {

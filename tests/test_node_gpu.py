@@ -43,6 +43,18 @@ def test_reference_call_forms_through_node(tmp_path):
                   "kv": [_save(d, "kv0.bin", kv[0, :77]), _save(d, "kv1.bin", kv[1, :1])]})
     refs["dit_cross_loop"] = orc.reference_torch(c).reshape(2 * 256, 576)
 
+    s4 = workloads.dit_self(B=4, seed=14)
+    cases.append({"name": "dit_self_callsite", "form": "dit_self_callsite", "B": 4, "qkv": _save(d, "qkv4.bin", s4.q)})
+    refs["dit_self_callsite"] = orc.reference_torch(s4).reshape(4 * 256, 576)
+
+    lens = [77, 1, 50, 3]
+    c4 = workloads.dit_cross(B=4, key_len=lens, seed=15)
+    kv4 = c4.k.reshape(4, 128, 1152)
+    cases.append({"name": "dit_cross_callsite", "form": "dit_cross_callsite", "B": 4, "L": lens,
+                  "q": _save(d, "cq4.bin", c4.q),
+                  "kv": [_save(d, f"kv4_{b}.bin", kv4[b, :lens[b]]) for b in range(4)]})
+    refs["dit_cross_callsite"] = orc.reference_torch(c4).reshape(4 * 256, 576)
+
     t5 = workloads.t5_self(seed=12, masked_tail=0)
     t5_files = {"q": _save(d, "t5q.bin", t5.q), "k": _save(d, "t5k.bin", t5.k), "v": _save(d, "t5v.bin", t5.v),
                 "table": _save(d, "t5t.bin", t5.bias)}
