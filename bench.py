@@ -153,6 +153,51 @@ def callsite_block(dev, s_st, c_st, reps: int = 20) -> dict:
     return out
 
 
+def linear_block(dev, B: int = 64, reps: int = 20, cpu: bool = True) -> dict:
+    """The six linears of one DiT block at batch B (app/models/dit.js:167-193: qkv, proj, q, cproj,
+    fc1, fc2 at B*256 rows) through sa_linear_f32: per-layer us, TFLOP/s and kernel, and the block
+    total; with cpu, the PyTorch fp32 CPU time of the same block (torch.mm + epilogue)."""
+    from supra_attn.linear_workloads import dit_block_linears
+    from supra_attn.runner import StagedLinear
+
+    calls = dit_block_linears(B=B)
+    staged = [StagedLinear(dev, c) for c in calls]
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 0.1:  # clocks settle
+        for st in staged:
+            st.launch()
+        dev.sync()
+    layers = {}
+    total_us = 0.0
+    for st in staged:
+        ms = time_calls(dev, st.launch, reps, warmup=2)
+        tf = st.call.flops() / (ms * 1e-3) / 1e12
+        total_us += ms * 1e3
+        layers[st.call.name] = {"shape": [st.call.M, st.call.N, st.call.K], "kernel": st.kernel,
+                                "us": round(ms * 1e3, 2), "tflops": round(tf, 2), "frac_peak": round(tf / PEAK_TFLOPS, 4)}
+    for st in staged:
+        st.release()
+    flops = sum(c.flops() for c in calls)
+    out = {"workload": f"one DiT block's linears at batch {B} ({B * 256} rows): qkv, proj (gated residual), q, "
+                       "cproj (residual), fc1 (GELU tanh), fc2 (gated residual)",
+           "layers": layers, "block_us": round(total_us, 2),
+           "block_tflops": round(flops / (total_us * 1e-6) / 1e12, 2),
+           "block_frac_peak": round(flops / (total_us * 1e-6) / 1e12 / PEAK_TFLOPS, 4)}
+    if cpu:
+        import torch
+
+        from oracle import linear as ol
+
+        t0 = time.perf_counter()
+        for c in calls:
+            ol.linear_torch_fp32(c.x, c.w, c.y0, **c.oracle_kwargs())
+        dt = time.perf_counter() - t0
+        out["cpu_baseline"] = {"ms_per_block": round(dt * 1e3, 1), "tflops": round(flops / dt / 1e12, 4),
+                               "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": "one block (6 layers) through oracle.linear.linear_torch_fp32 (torch.mm)"}
+    return out
+
+
 COPY_BYTES = 256 << 20
 
 
@@ -164,12 +209,19 @@ def profile_run(workload: str, launches: int) -> int:
     from supra_attn.runner import Staged
 
     dev = Device(0)
-    if workload in ("sweep_self", "sweep_cross"):
+    if workload.startswith("linear_"):
+        from supra_attn.linear_workloads import dit_block_linears
+        from supra_attn.runner import StagedLinear
+
+        call = [c for c in dit_block_linears(B=64) if c.name == workload[len("linear_"):]][0]
+        st = StagedLinear(dev, call)
+    elif workload in ("sweep_self", "sweep_cross"):
         s, c = workloads.SweepData(blocks=1).block(0)
         call = s if workload == "sweep_self" else c
+        st = Staged(dev, call)
     else:
         call = workloads.CONFIGS[workload]()
-    st = Staged(dev, call)
+        st = Staged(dev, call)
     log(f"profile {workload}: {launches} launches of {st.kernel}, "
         f"{call.flops()} flop and {call.algorithmic_bytes()} algorithmic bytes per launch")
     for _ in range(launches):
@@ -269,6 +321,11 @@ def main() -> int:
     log(f"call sites, one block: per-sample {callsite['per_sample_us']:.1f} us ({callsite['per_sample_launches']} "
         f"launches) vs batched {callsite['batched_us']:.1f} us (2 launches): {callsite['speedup']:.2f}x")
 
+    # the linears either side of attention in the same DiT block
+    linear = linear_block(dev, cpu=not args.no_cpu)
+    log(f"linears, one block at batch 64: {linear['block_us']:.1f} us, {linear['block_tflops']:.1f} TFLOP/s "
+        + " ".join(f"{k} {v['us']:.0f}us" for k, v in linear["layers"].items()))
+
     # single-call configs
     per_config = {}
     for name, make in workloads.CONFIGS.items():
@@ -345,6 +402,7 @@ def main() -> int:
         "per_config": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                        for k, v in per_config.items()},
         "callsite": callsite,
+        "linear": linear,
         "cpu_baseline": None if cpu is None else {k: (round(v, 6) if isinstance(v, float) else v) for k, v in cpu.items()},
     }
     print(json.dumps(result))

@@ -1,5 +1,5 @@
-// C ABI of the attention operator: argument validation, kernel selection and the device-runtime
-// helpers the JS addon and the Python bindings use.
+// C ABI of the attention operator and the linear layer: argument validation, kernel selection and
+// the device-runtime helpers the JS addon and the Python bindings use.
 //
 // The operator contract follows app/gpu/ops.js:103-149 (offsets/strides in floats, default output
 // row stride H*D, synchronous error for an unsupported request) extended with batch strides, a
@@ -15,6 +15,7 @@
 #include <string.h>
 
 #include "supra_attn.h"
+#include "supra_linear.h"
 #include "common.h"
 #include "kernels.h"
 
@@ -149,6 +150,53 @@ int resolve(const sa_attn_args* a, sa::AttnParams* p) {
   return SA_OK;
 }
 
+// Resolves an sa_linear_args (app/gpu/ops.js:35-43 semantics) into kernel parameters.
+int resolve_linear(const sa_linear_args* a, sa::LinearParams* p) {
+  if (a == nullptr) return fail(SA_ERR_INVALID, "args is NULL");
+  if (a->struct_size != sizeof(sa_linear_args))
+    return fail(SA_ERR_INVALID, "struct_size %u does not match sizeof(sa_linear_args) = %zu", a->struct_size,
+                sizeof(sa_linear_args));
+  if (a->M <= 0 || a->N <= 0 || a->K <= 0)
+    return fail(SA_ERR_INVALID, "M, N, K must be positive (got %d, %d, %d)", a->M, a->N, a->K);
+  if (!a->x || !a->w || !a->y) return fail(SA_ERR_INVALID, "x, w and y must be non-NULL device pointers");
+  if (a->x_off < 0 || a->y_off < 0 || a->gate_off < 0) return fail(SA_ERR_INVALID, "offsets must be >= 0");
+  const int64_t ldx = a->ldx ? a->ldx : a->K, ldw = a->ldw ? a->ldw : a->K, ldy = a->ldy ? a->ldy : a->N;
+  if (ldx < a->K || ldw < a->K)
+    return fail(SA_ERR_INVALID, "row strides of x and w must be >= K = %d (ldx=%lld ldw=%lld)", a->K, (long long)ldx,
+                (long long)ldw);
+  if (ldy < a->N) return fail(SA_ERR_INVALID, "row stride of y must be >= N = %d (ldy=%lld)", a->N, (long long)ldy);
+  if (!isfinite(a->alpha)) return fail(SA_ERR_INVALID, "alpha must be finite");
+  if (a->act < SA_ACT_NONE || a->act > SA_ACT_SILU) return fail(SA_ERR_INVALID, "unknown act %d", a->act);
+  if (a->epilogue < SA_EPI_STORE || a->epilogue > SA_EPI_RESID_GATE)
+    return fail(SA_ERR_INVALID, "unknown epilogue %d", a->epilogue);
+  if (a->epilogue == SA_EPI_RESID_GATE && !a->gate) return fail(SA_ERR_INVALID, "SA_EPI_RESID_GATE needs gate");
+  // the output must not overlap what the kernel reads (it reads y itself only at the element it writes)
+  const Extent ey = extent(a->y, a->y_off, 0, ldy, 1, a->M, a->N);
+  if (overlaps(ey, extent(a->x, a->x_off, 0, ldx, 1, a->M, a->K)) || overlaps(ey, extent(a->w, 0, 0, ldw, 1, a->N, a->K)))
+    return fail(SA_ERR_ALIAS, "y overlaps x or w");
+  if (a->bias && overlaps(ey, extent(a->bias, 0, 0, 0, 1, 1, a->N))) return fail(SA_ERR_ALIAS, "y overlaps bias");
+  if (a->epilogue == SA_EPI_RESID_GATE && overlaps(ey, extent(a->gate, a->gate_off, 0, 0, 1, 1, a->N)))
+    return fail(SA_ERR_ALIAS, "y overlaps gate");
+  p->x = a->x;
+  p->x_off = a->x_off;
+  p->ldx = ldx;
+  p->w = a->w;
+  p->ldw = ldw;
+  p->bias = a->bias;
+  p->gate = a->epilogue == SA_EPI_RESID_GATE ? a->gate : nullptr;
+  p->gate_off = a->gate_off;
+  p->y = a->y;
+  p->y_off = a->y_off;
+  p->ldy = ldy;
+  p->M = a->M;
+  p->N = a->N;
+  p->K = a->K;
+  p->alpha = a->alpha;
+  p->act = a->act;
+  p->epi = a->epilogue;
+  return SA_OK;
+}
+
 enum class Path { kFlash, kWide, kGeneric };
 
 struct Choice {
@@ -270,6 +318,22 @@ int64_t sa_attention_workspace_bytes(const sa_attn_args* args) {
   if (rc != SA_OK) return rc;
   ok();
   return c.path == Path::kWide ? c.wide.ws_floats * (int64_t)sizeof(float) : 0;
+}
+
+int sa_linear_f32(const sa_linear_args* args, void* stream) {
+  sa::LinearParams p;
+  const int rc = resolve_linear(args, &p);
+  if (rc != SA_OK) return rc;
+  const hipError_t e = sa::launch_linear(p, num_cus(), (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, sa::linear_kernel_name(p, num_cus()));
+  return ok();
+}
+
+const char* sa_linear_kernel_name(const sa_linear_args* args) {
+  sa::LinearParams p;
+  if (resolve_linear(args, &p) != SA_OK) return nullptr;
+  ok();
+  return sa::linear_kernel_name(p, num_cus());
 }
 
 const char* sa_attention_kernel_name(const sa_attn_args* args) {

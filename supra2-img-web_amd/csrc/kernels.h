@@ -60,4 +60,30 @@ hipError_t launch_position_bias(const float* table, const int32_t* lut, int num_
 
 constexpr int GENERIC_MAX_D = 1024;
 
+// ---- linear layer y = epilogue(alpha * x W^T) (csrc/linear_mfma.hip)
+enum { LIN_ACT_NONE = 0, LIN_ACT_GELU = 1, LIN_ACT_GELU_TANH = 2, LIN_ACT_SILU = 3 };
+enum { LIN_EPI_STORE = 0, LIN_EPI_RESID = 1, LIN_EPI_RESID_GATE = 2 };
+struct LinearParams {
+  const float* x;  // [M, K] rows at x + x_off + m*ldx
+  int64_t x_off, ldx;
+  const float* w;  // [N, K] rows at w + n*ldw
+  int64_t ldw;
+  const float* bias;  // [N] or null
+  const float* gate;  // gate[gate_off + n] (LIN_EPI_RESID_GATE)
+  int64_t gate_off;
+  float* y;  // [M, N] rows at y + y_off + m*ldy
+  int64_t y_off, ldy;
+  int M, N, K;
+  float alpha;
+  int act, epi;
+};
+struct LinearTile {
+  int wm, wn;  // 32x32 accumulators per wave along M and N (tile 64*wm x 64*wn)
+};
+// MFMA kernel when K % 8 == 0 and x, W rows are 16-byte aligned; the generic kernel otherwise.
+bool linear_mfma_supported(const LinearParams& p);
+LinearTile linear_mfma_tile(const LinearParams& p, int num_cus);
+const char* linear_kernel_name(const LinearParams& p, int num_cus);
+hipError_t launch_linear(const LinearParams& p, int num_cus, hipStream_t stream);
+
 }  // namespace sa

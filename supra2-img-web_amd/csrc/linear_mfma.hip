@@ -1,0 +1,393 @@
+// Linear layer y = epilogue(alpha * x W^T) on fp32 MFMA for gfx950: the projections either side of
+// the attention operator (app/gpu/ops.js:35-43 `linear`, app/gpu/gemm.js:116-223 `matmulShader`
+// with A mode "rows" and B format "f32"): the DiT qkv / proj / q / kv / cproj / fc1 / fc2 layers.
+//
+//   x [M, K] rows at x + x_off + m*ldx;  W [N, K] (PyTorch layout) rows at w + n*ldw
+//   r = alpha * sum_k x[m][k] W[n][k] (+ bias[n]), then act (GELU erf / GELU tanh / SiLU), then
+//   y[m][n] = r, y[m][n] += r, or y[m][n] += gate[gate_off + n] * r (gemm.js:127-137).
+//
+// Work decomposition
+//   A workgroup is 4 wave64s in a 2 x 2 grid computing a BM x BN tile (BM = 64*WM, BN = 64*WN);
+//   each wave owns (32*WM) x (32*WN) outputs as WM x WN 32x32 accumulators of
+//   v_mfma_f32_32x32x2f32. The x rows are the MFMA A operand and the W rows the B operand, so
+//   lane l of an accumulator holds column n = l%32 and rows 8*(r/4) + 4*(l/32) + r%4 of register r:
+//   every store instruction writes 128 contiguous bytes of two rows.
+//   K advances in tiles of BK. Within a group of 8 consecutive k, half-wave h supplies
+//   k = 8g + 4h + s at MFMA step s (s = 0..3): one b128 LDS read per operand row and group feeds
+//   four MFMAs, and every (x, W) pair of k meets exactly once.
+//
+// Tiles move HBM/L2 -> LDS with global_load_lds_dwordx4 (no VGPR staging), NS stages, one barrier
+// per k-tile. LDS rows are BK floats (BK/4 chunks of 16 bytes); chunk c of row r sits at
+// c ^ ((r / RP) % (BK/4)) with RP = 64/BK rows per 256 bytes, which makes the b128 operand reads of
+// 16 consecutive rows conflict-free (measured SQ_LDS_BANK_CONFLICT = 0). The operands of the next
+// group of 8 k are read from LDS while the MFMAs of the current group run, and the barrier of the
+// next k-tile sits before the last group's MFMAs.
+//
+// The epilogue shares the SIMD datapath with the fp32 MFMAs, so it is kept short: activation and
+// store mode are template parameters (no per-element branches), stores are raw buffer stores with
+// scalar descriptors and row offsets, whole tiles skip the bounds checks.
+// Rows past M (x) or N (W) re-read the last row (finite data, never stored); the k-tile holding K
+// clamps its column to K - 8 and only its valid groups of 8 are multiplied (K % 8 == 0).
+//
+// Consecutive tiles along N share the x row block: the tile order (x row block major, remapped so
+// that consecutive tiles run on one XCD) keeps that block in the XCD's L2 while its N tiles run.
+
+#include <type_traits>
+
+#include "common.h"
+#include "kernels.h"
+
+namespace sa {
+
+namespace {
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) const void global_void_t;
+
+__device__ __forceinline__ void load_to_lds16(const void* src, float* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)lds_wave_base, 16, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+// Activations of app/gpu/gemm.js:21-36. The epilogue runs on the same SIMD datapath as the fp32
+// MFMAs, so the two logistic forms use one hardware exp2 and one reciprocal:
+//   GELU (tanh) 0.5 x (1 + tanh(u)) = x / (1 + e^(-2u)),  u = sqrt(2/pi) (x + 0.044715 x^3);
+//   SiLU        x / (1 + e^(-x)).
+// Both saturate correctly: e^(...) -> inf gives x * 0, e^(...) -> 0 gives x. GELU (erf) calls erff.
+__device__ __forceinline__ float logistic_times(float x, float z) {  // x / (1 + e^z)
+  return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(z * kLog2e));
+}
+
+template <int ACT>
+__device__ __forceinline__ float apply_act(float v) {
+  if constexpr (ACT == LIN_ACT_GELU) return 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
+  if constexpr (ACT == LIN_ACT_GELU_TANH) {
+    const float u = v * fmaf(0.035677408136300125f, v * v, 0.79788456080286536f);  // sqrt(2/pi) * (1, 0.044715)
+    return logistic_times(v, -2.f * u);
+  }
+  if constexpr (ACT == LIN_ACT_SILU) return logistic_times(v, -v);
+  return v;
+}
+
+// s_waitcnt with vmcnt <= N (expcnt and lgkmcnt left unconstrained), gfx9 encoding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// WM x WN accumulators per wave, BK k per tile (16 or 32), NS tiles in flight (LDS stages); the
+// activation and the epilogue are compile-time, so the store loop has no per-element branches.
+template <int WM, int WN, int BK, int NS, int ACT, int EPI>
+__global__ __launch_bounds__(256, 2) void linear_mfma_kernel(LinearParams p, int tiles_n) {
+  constexpr int BM = 64 * WM;
+  constexpr int BN = 64 * WN;
+  constexpr int CPR = BK / 4;            // 16-byte chunks per tile row
+  constexpr int RP = 64 / BK;            // tile rows per 256 bytes (one pass over the 64 banks)
+  constexpr int NG = BK / 8;             // groups of 8 k per tile
+  constexpr int A_TILE = BM * BK;        // floats per stage
+  constexpr int B_TILE = BN * BK;
+  constexpr int STAGE = A_TILE + B_TILE;
+  constexpr int NIA = BM * CPR / 256;    // DMA instructions per wave and stage (64 chunks each)
+  constexpr int NIB = BN * CPR / 256;
+  constexpr int NI = NIA + NIB;
+  static_assert(NIA * 256 == BM * CPR && NIB * 256 == BN * CPR, "tiles must split into whole wave copies");
+  static_assert(NS == 2 || NS == 3, "two or three stages");
+  static_assert(NG % 2 == 0, "an even number of groups per tile");
+
+  __shared__ __attribute__((aligned(16))) float lds[NS * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
+  const int col = lane & 31;
+  const int half = lane >> 5;
+
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int m0 = (tile / tiles_n) * BM;
+  const int n0 = (tile % tiles_n) * BN;
+
+  const float* xbase = p.x + p.x_off + (int64_t)m0 * p.ldx;
+  const float* wbase = p.w + (int64_t)n0 * p.ldw;
+  const int mlast = min(BM, p.M - m0) - 1;  // last valid tile row
+  const int nlast = min(BN, p.N - n0) - 1;
+
+  // Per-lane byte offsets (from the tile's first row at k = 0) of this lane's 16-byte chunk in
+  // each DMA instruction: instruction n of wave w fills physical chunks (n*4 + w)*64 + lane; the
+  // chunk c of row r sits at physical chunk c ^ ((r / RP) % CPR).
+  unsigned aoff[NIA], boff[NIB];
+  int acol[NIA], bcol[NIB];  // logical column (floats) of the chunk, for the clamped k-tile
+#pragma unroll
+  for (int n = 0; n < NIA; ++n) {
+    const int pc_all = (n * 4 + wave) * 64 + lane;
+    const int row = pc_all / CPR;
+    const int c = (pc_all % CPR) ^ ((row / RP) % CPR);
+    acol[n] = 4 * c;
+    aoff[n] = 4u * (unsigned)(min(row, mlast) * (int)p.ldx + 4 * c);
+  }
+#pragma unroll
+  for (int n = 0; n < NIB; ++n) {
+    const int pc_all = (n * 4 + wave) * 64 + lane;
+    const int row = pc_all / CPR;
+    const int c = (pc_all % CPR) ^ ((row / RP) % CPR);
+    bcol[n] = 4 * c;
+    boff[n] = 4u * (unsigned)(min(row, nlast) * (int)p.ldw + 4 * c);
+  }
+
+  const int nkt = (p.K + BK - 1) / BK;
+  auto issue = [&](int kt) {
+    float* at = lds + (kt % NS) * STAGE;
+    float* bt = at + A_TILE;
+    const int k0 = kt * BK;
+    const char* xa = reinterpret_cast<const char*>(xbase + k0);
+    const char* wb = reinterpret_cast<const char*>(wbase + k0);
+    if (k0 + BK <= p.K) {
+#pragma unroll
+      for (int n = 0; n < NIA; ++n) load_to_lds16(xa + aoff[n], at + (n * 4 + wave) * 256);
+#pragma unroll
+      for (int n = 0; n < NIB; ++n) load_to_lds16(wb + boff[n], bt + (n * 4 + wave) * 256);
+    } else {
+      // the k-tile holding K: columns at or past K re-read the last group (never multiplied)
+      const int kmax = p.K - 8 - k0;
+#pragma unroll
+      for (int n = 0; n < NIA; ++n) {
+        const int shift = acol[n] > kmax + 4 ? (acol[n] & ~7) - kmax : 0;  // whole groups back
+        load_to_lds16(xa + aoff[n] - 4 * shift, at + (n * 4 + wave) * 256);
+      }
+#pragma unroll
+      for (int n = 0; n < NIB; ++n) {
+        const int shift = bcol[n] > kmax + 4 ? (bcol[n] & ~7) - kmax : 0;
+        load_to_lds16(wb + boff[n] - 4 * shift, bt + (n * 4 + wave) * 256);
+      }
+    }
+  };
+
+  f32x16 acc[WM][WN];
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int j = 0; j < WN; ++j) acc[i][j] = zero16();
+
+  // LDS read offsets (floats) of this lane's operand chunk in group g: row (32*i + col) of the
+  // wave's block, logical chunk 2g + half; the swizzle depends on the row only through col
+  const int swz = (col / RP) % CPR;
+  int goff[NG];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) goff[g] = col * BK + 4 * ((2 * g + half) ^ swz);
+  const int arow0 = wm * 32 * WM * BK;  // wave's first A row, in floats
+  const int brow0 = wn * 32 * WN * BK;
+
+  // Operands of one group in registers, double-buffered: group g + 1 (or group 0 of the next
+  // tile) is read from LDS while the MFMAs of group g run.
+  f32x4 ra[2][WM], rb[2][WN];
+  auto read_group = [&](int kt, int g, int slot) {
+    const float* at = lds + (kt % NS) * STAGE + arow0 + goff[g];
+    const float* bt = lds + (kt % NS) * STAGE + A_TILE + brow0 + goff[g];
+#pragma unroll
+    for (int i = 0; i < WM; ++i) ra[slot][i] = *reinterpret_cast<const f32x4*>(at + i * 32 * BK);
+#pragma unroll
+    for (int j = 0; j < WN; ++j) rb[slot][j] = *reinterpret_cast<const f32x4*>(bt + j * 32 * BK);
+  };
+  // tile kt has landed for this thread (the younger tiles may still be in flight); the barrier
+  // makes it whole and guarantees every wave has read the stage the next copies overwrite
+  auto sync_tile = [&](int kt) {
+    if (NS == 3 && kt + 1 < nkt) {
+      wait_vmcnt<(NS == 3 ? NI : 0)>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    __syncthreads();
+    if (kt + NS - 1 < nkt) issue(kt + NS - 1);
+  };
+
+#pragma unroll
+  for (int t = 0; t < NS - 1; ++t)
+    if (t < nkt) issue(t);
+  sync_tile(0);
+  read_group(0, 0, 0);
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int ng = min(NG, (p.K - kt * BK) >> 3);  // valid groups of 8 k in this tile
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const int cur = g & 1;  // NG is even, so group 0 of every tile sits in slot 0
+      if (g + 1 < NG) {
+        read_group(kt, g + 1, cur ^ 1);
+      } else if (kt + 1 < nkt) {
+        sync_tile(kt + 1);
+        read_group(kt + 1, 0, cur ^ 1);
+      }
+      if (g < ng) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+          for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(ra[cur][i][s], rb[cur][j][s], acc[i][j], 0, 0, 0);
+      }
+    }
+  }
+
+  // ---- epilogue: lane holds column n = nw + 32j + col, rows mw + 32i + 8(r/4) + 4*half + r%4.
+  // Buffer loads/stores over the wave's output block: a scalar descriptor, a 32-bit per-lane
+  // offset and a scalar per-row offset (no 64-bit address arithmetic per element); whole tiles
+  // skip the bounds checks.
+  const int mw = m0 + wm * 32 * WM;
+  const int nw = n0 + wn * 32 * WN;
+  const bool full = m0 + BM <= p.M && n0 + BN <= p.N;
+  const __amdgpu_buffer_rsrc_t yr =
+      __builtin_amdgcn_make_buffer_rsrc(p.y + p.y_off + (int64_t)mw * p.ldy + nw, 0, 0x7fffffff, 0x00020000);
+  const int ldy4 = 4 * (int)p.ldy;
+  auto store = [&](auto check) {
+    constexpr bool kCheck = decltype(check)::value;
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const int nl = 32 * j + col;
+      const bool n_ok = !kCheck || nw + nl < p.N;
+      const float bias_n = (p.bias && n_ok) ? p.bias[nw + nl] : 0.f;
+      float gate_n = 1.f;
+      if constexpr (EPI == LIN_EPI_RESID_GATE) gate_n = n_ok ? p.gate[p.gate_off + nw + nl] : 0.f;
+#pragma unroll
+      for (int i = 0; i < WM; ++i) {
+        const int voff = (32 * i + 4 * half) * ldy4 + 4 * nl;
+        // residual epilogues: the 16 old values of the block are loaded together, then combined
+        float old[16];
+        if constexpr (EPI != LIN_EPI_STORE) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int rr = 8 * (r >> 2) + (r & 3);
+            old[r] = 0.f;
+            if (!kCheck || (n_ok && mw + 32 * i + 4 * half + rr < p.M))
+              old[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(yr, voff, rr * ldy4, 0));
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int rr = 8 * (r >> 2) + (r & 3);
+          if (!kCheck || (n_ok && mw + 32 * i + 4 * half + rr < p.M)) {
+            float v = apply_act<ACT>(fmaf(acc[i][j][r], p.alpha, bias_n));
+            if constexpr (EPI != LIN_EPI_STORE) v = fmaf(gate_n, v, old[r]);
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), yr, voff, rr * ldy4, 0);
+          }
+        }
+      }
+    }
+  };
+  if (full) {
+    store(std::false_type{});
+  } else {
+    store(std::true_type{});
+  }
+}
+
+// Any shape and alignment: one thread per output, 16 x 16 outputs per workgroup, K in steps of
+// 16 through LDS. Used when rows are not 16-byte aligned or K % 8 != 0.
+__global__ __launch_bounds__(256) void linear_generic_kernel(LinearParams p) {
+  __shared__ float xs[16][17];
+  __shared__ float ws[16][17];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int m = blockIdx.y * 16 + ty;
+  const int n = blockIdx.x * 16 + tx;
+  const int mload = blockIdx.y * 16 + ty;  // row loaded by this thread (x tile)
+  const int nload = blockIdx.x * 16 + ty;  // row loaded by this thread (W tile)
+  float acc = 0.f;
+  for (int k0 = 0; k0 < p.K; k0 += 16) {
+    const int k = k0 + tx;
+    xs[ty][tx] = (mload < p.M && k < p.K) ? p.x[p.x_off + (int64_t)mload * p.ldx + k] : 0.f;
+    ws[ty][tx] = (nload < p.N && k < p.K) ? p.w[(int64_t)nload * p.ldw + k] : 0.f;
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) acc = fmaf(xs[ty][kk], ws[tx][kk], acc);
+    __syncthreads();
+  }
+  if (m < p.M && n < p.N) {
+    float v = fmaf(acc, p.alpha, p.bias ? p.bias[n] : 0.f);
+    switch (p.act) {
+      case LIN_ACT_GELU: v = apply_act<LIN_ACT_GELU>(v); break;
+      case LIN_ACT_GELU_TANH: v = apply_act<LIN_ACT_GELU_TANH>(v); break;
+      case LIN_ACT_SILU: v = apply_act<LIN_ACT_SILU>(v); break;
+      default: break;
+    }
+    float* dst = p.y + p.y_off + (int64_t)m * p.ldy + n;
+    if (p.epi == LIN_EPI_STORE) *dst = v;
+    else *dst = fmaf(p.epi == LIN_EPI_RESID_GATE ? p.gate[p.gate_off + n] : 1.f, v, *dst);
+  }
+}
+
+template <int WM, int WN, int BK, int NS, int ACT, int EPI>
+hipError_t launch_tiles(const LinearParams& p, hipStream_t stream) {
+  const int64_t tm = (p.M + 64 * WM - 1) / (64 * WM);
+  const int64_t tn = (p.N + 64 * WN - 1) / (64 * WN);
+  if (tm * tn > 0x7fffffff) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL((linear_mfma_kernel<WM, WN, BK, NS, ACT, EPI>), dim3((unsigned)(tm * tn)), dim3(256), 0, stream, p,
+                     (int)tn);
+  return hipGetLastError();
+}
+
+template <int WM, int WN, int BK, int NS, int ACT>
+hipError_t launch_epi(const LinearParams& p, hipStream_t stream) {
+  switch (p.epi) {
+    case LIN_EPI_STORE: return launch_tiles<WM, WN, BK, NS, ACT, LIN_EPI_STORE>(p, stream);
+    case LIN_EPI_RESID: return launch_tiles<WM, WN, BK, NS, ACT, LIN_EPI_RESID>(p, stream);
+    case LIN_EPI_RESID_GATE: return launch_tiles<WM, WN, BK, NS, ACT, LIN_EPI_RESID_GATE>(p, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int WM, int WN, int BK, int NS>
+hipError_t launch_act(const LinearParams& p, hipStream_t stream) {
+  switch (p.act) {
+    case LIN_ACT_NONE: return launch_epi<WM, WN, BK, NS, LIN_ACT_NONE>(p, stream);
+    case LIN_ACT_GELU: return launch_epi<WM, WN, BK, NS, LIN_ACT_GELU>(p, stream);
+    case LIN_ACT_GELU_TANH: return launch_epi<WM, WN, BK, NS, LIN_ACT_GELU_TANH>(p, stream);
+    case LIN_ACT_SILU: return launch_epi<WM, WN, BK, NS, LIN_ACT_SILU>(p, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+bool linear_mfma_supported(const LinearParams& p) {
+  auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  return p.K % 8 == 0 && a16(p.x) && a16(p.w) && p.x_off % 4 == 0 && p.ldx % 4 == 0 && p.ldw % 4 == 0 &&
+         (int64_t)64 * 2 * p.ldx * 4 < 0x7fffffffLL && (int64_t)64 * 3 * p.ldw * 4 < 0x7fffffffLL &&
+         (int64_t)64 * 2 * p.ldy < 0x7fffffffLL;
+}
+
+LinearTile linear_mfma_tile(const LinearParams& p, int num_cus) {
+  // Measured on the DiT layers at 16384 rows (after a warm-up, per layer): wide outputs run best
+  // on 128 x 192 tiles (qkv N = 1728: 282 us vs 286 for 128 x 64; fc1 N = 2304: 350 vs 371), the
+  // 576-wide ones on 128 x 64 tiles at three workgroups per CU (proj/q/cproj: 106 vs 120 us; fc2:
+  // 404 vs 452). Narrow tiles also keep small-M calls spread over the CUs.
+  const int64_t tiles_wide = ((p.M + 127) / 128) * ((p.N + 191) / 192);
+  if (p.N >= 1024 && tiles_wide >= num_cus) return {2, 3};
+  return {2, 1};
+}
+
+const char* linear_kernel_name(const LinearParams& p, int num_cus) {
+  if (!linear_mfma_supported(p)) return "linear_generic";
+  const LinearTile t = linear_mfma_tile(p, num_cus);
+  return t.wn == 3 ? "linear_mfma_128x192" : "linear_mfma_128x64";
+}
+
+hipError_t launch_linear(const LinearParams& p, int num_cus, hipStream_t stream) {
+  if (!linear_mfma_supported(p)) {
+    const dim3 grid((unsigned)((p.N + 15) / 16), (unsigned)((p.M + 15) / 16));
+    if ((p.N + 15) / 16 > 0x7fffffff || (p.M + 15) / 16 > 65535) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL(linear_generic_kernel, grid, dim3(256), 0, stream, p);
+    return hipGetLastError();
+  }
+  const LinearTile t = linear_mfma_tile(p, num_cus);
+  if (t.wn == 3) return launch_act<2, 3, 32, 2>(p, stream);
+  return launch_act<2, 1, 32, 2>(p, stream);
+}
+
+}  // namespace sa

@@ -19,6 +19,7 @@
 #include <string.h>
 
 #include "supra_attn.h"
+#include "supra_linear.h"
 
 static void* g_stream = NULL;
 static int g_stream_ready = 0;
@@ -204,6 +205,73 @@ static int fill_args(napi_env env, napi_value o, sa_attn_args* a) {
   a->key_mask = (const uint8_t*)km;
   a->workspace = ws;
   return 0;
+}
+
+/* opts -> sa_linear_args: M, N, K, x, xOff, ldx, w, ldw, bias, alpha (default 1), act, epilogue,
+ * gate, gateOff, y, yOff, ldy (the JS shim maps app/gpu/ops.js:35-43's linear() onto these). */
+static int fill_linear(napi_env env, napi_value o, sa_linear_args* a) {
+  memset(a, 0, sizeof *a);
+  a->struct_size = sizeof *a;
+  int64_t M, N, K, act, epi;
+  void *x, *w, *bias, *gate, *y;
+  double alpha;
+  napi_value av;
+  if (prop_i64(env, o, "M", -1, &M) || prop_i64(env, o, "N", -1, &N) || prop_i64(env, o, "K", -1, &K) ||
+      prop_i64(env, o, "act", SA_ACT_NONE, &act) || prop_i64(env, o, "epilogue", SA_EPI_STORE, &epi) ||
+      prop_i64(env, o, "xOff", 0, &a->x_off) || prop_i64(env, o, "ldx", 0, &a->ldx) ||
+      prop_i64(env, o, "ldw", 0, &a->ldw) || prop_i64(env, o, "gateOff", 0, &a->gate_off) ||
+      prop_i64(env, o, "yOff", 0, &a->y_off) || prop_i64(env, o, "ldy", 0, &a->ldy))
+    return 1;
+  if (prop_ptr(env, o, "x", &x) || prop_ptr(env, o, "w", &w) || prop_ptr(env, o, "bias", &bias) ||
+      prop_ptr(env, o, "gate", &gate) || prop_ptr(env, o, "y", &y))
+    return 1;
+  if (prop(env, o, "alpha", &av) || get_f64(env, av, 1.0, &alpha, "alpha")) return 1;
+  if (M > 0x7fffffffLL || N > 0x7fffffffLL || K > 0x7fffffffLL || M < -1 || N < -1 || K < -1) {
+    napi_throw_range_error(env, "SA_ERR_INVALID", "sizes must fit in int32");
+    return 1;
+  }
+  a->M = (int32_t)M;
+  a->N = (int32_t)N;
+  a->K = (int32_t)K;
+  a->x = (const float*)x;
+  a->w = (const float*)w;
+  a->bias = (const float*)bias;
+  a->alpha = (float)alpha;
+  a->act = (int32_t)act;
+  a->epilogue = (int32_t)epi;
+  a->gate = (const float*)gate;
+  a->y = (float*)y;
+  return 0;
+}
+
+static napi_value js_linear(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (get_args(env, info, 1, argv)) return NULL;
+  sa_linear_args a;
+  if (fill_linear(env, argv[0], &a)) return NULL;
+  /* validate before touching the device, so a bad call reports its own error on any host */
+  if (sa_linear_kernel_name(&a) == NULL) {
+    throw_if(env, SA_ERR_INVALID);
+    return NULL;
+  }
+  if (ensure_stream(env)) return NULL;
+  if (throw_if(env, sa_linear_f32(&a, g_stream))) return NULL;
+  return undefined(env);
+}
+
+static napi_value js_linear_kernel_name(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (get_args(env, info, 1, argv)) return NULL;
+  sa_linear_args a;
+  if (fill_linear(env, argv[0], &a)) return NULL;
+  const char* name = sa_linear_kernel_name(&a);
+  if (!name) {
+    throw_if(env, SA_ERR_INVALID);
+    return NULL;
+  }
+  napi_value r;
+  NAPI_CALL(env, napi_create_string_utf8(env, name, NAPI_AUTO_LENGTH, &r));
+  return r;
 }
 
 static napi_value js_attention(napi_env env, napi_callback_info info) {
@@ -492,6 +560,8 @@ static napi_value init(napi_env env, napi_value exports) {
       {"attention", NULL, js_attention, NULL, NULL, NULL, napi_enumerable, NULL},
       {"kernelName", NULL, js_kernel_name, NULL, NULL, NULL, napi_enumerable, NULL},
       {"workspaceBytes", NULL, js_workspace_bytes, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"linear", NULL, js_linear, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"linearKernelName", NULL, js_linear_kernel_name, NULL, NULL, NULL, napi_enumerable, NULL},
       {"version", NULL, js_version, NULL, NULL, NULL, napi_enumerable, NULL},
       {"deviceCount", NULL, js_device_count, NULL, NULL, NULL, napi_enumerable, NULL},
       {"malloc", NULL, js_malloc, NULL, NULL, NULL, napi_enumerable, NULL},

@@ -1,10 +1,11 @@
-// Entry point of the JS binding: the device runtime, the attention operator and the batched DiT
-// call sites.
+// Entry point of the JS binding: the device runtime, the attention operator, the batched DiT call
+// sites and the linear layer either side of attention.
 "use strict";
 
 var device = require("./device");
 var ops = require("./ops");
 var dit = require("./dit_attn");
+var lin = require("./linear");
 
 module.exports = {
   GPU: device.GPU,
@@ -16,4 +17,6 @@ module.exports = {
   relposBias: ops.relposBias,
   positionBias: ops.positionBias,
   dit: dit,
+  linear: lin.linear,
+  linearKernel: lin.linearKernel,
 };

@@ -9,6 +9,6 @@ The operator itself is HIP code behind the C ABI in include/supra_attn.h
 - `runner`    stage a workload on the device and launch it
 """
 
-from ._lib import AttnArgs, SaError, attention, bucket_lut, kernel_name, load, workspace_bytes  # noqa: F401
+from ._lib import AttnArgs, LinearArgs, SaError, attention, bucket_lut, kernel_name, linear, load, workspace_bytes  # noqa: F401
 
-__all__ = ["AttnArgs", "SaError", "attention", "bucket_lut", "kernel_name", "load", "workspace_bytes"]
+__all__ = ["AttnArgs", "LinearArgs", "SaError", "attention", "bucket_lut", "kernel_name", "linear", "load", "workspace_bytes"]

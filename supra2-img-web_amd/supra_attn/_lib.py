@@ -1,4 +1,4 @@
-"""ctypes binding of libsupra_attn.so (include/supra_attn.h).
+"""ctypes binding of libsupra_attn.so (include/supra_attn.h, include/supra_linear.h).
 
 Loading fails loudly when the library has not been built: there is no other implementation of the
 operator behind this module.
@@ -27,11 +27,22 @@ SA_MASK_NONE = 0
 SA_MASK_KEY_LEN = 1
 SA_MASK_KEY_MASK = 2
 
+SA_ACT_NONE = 0
+SA_ACT_GELU = 1
+SA_ACT_GELU_TANH = 2
+SA_ACT_SILU = 3
+
+SA_EPI_STORE = 0
+SA_EPI_RESID = 1
+SA_EPI_RESID_GATE = 2
+
 # Every symbol include/supra_attn.h declares, with (restype, argtypes).
 SIGNATURES = {
     "sa_attention_f32": (c_int, [c_void_p, c_void_p]),
     "sa_attention_kernel_name": (c_char_p, [c_void_p]),
     "sa_attention_workspace_bytes": (c_int64, [c_void_p]),
+    "sa_linear_f32": (c_int, [c_void_p, c_void_p]),
+    "sa_linear_kernel_name": (c_char_p, [c_void_p]),
     "sa_t5_bucket_lut": (c_int, [c_int32, c_int32, c_int32, c_int32, c_int32, POINTER(c_int32)]),
     "sa_t5_position_bias": (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p]),
     "sa_device_count": (c_int, [POINTER(c_int32)]),
@@ -111,6 +122,38 @@ class AttnArgs(ctypes.Structure):
             setattr(self, name, val)
 
 
+class LinearArgs(ctypes.Structure):
+    """Mirror of sa_linear_args (include/supra_linear.h); alpha defaults to 1."""
+
+    _fields_ = [
+        ("struct_size", c_uint32),
+        ("M", c_int32),
+        ("N", c_int32),
+        ("K", c_int32),
+        ("x", c_void_p),
+        ("x_off", c_int64),
+        ("ldx", c_int64),
+        ("w", c_void_p),
+        ("ldw", c_int64),
+        ("bias", c_void_p),
+        ("alpha", c_float),
+        ("act", c_int32),
+        ("epilogue", c_int32),
+        ("gate", c_void_p),
+        ("gate_off", c_int64),
+        ("y", c_void_p),
+        ("y_off", c_int64),
+        ("ldy", c_int64),
+    ]
+
+    def __init__(self, **kw):
+        super().__init__()
+        self.struct_size = ctypes.sizeof(LinearArgs)
+        self.alpha = 1.0
+        for name, val in kw.items():
+            setattr(self, name, val)
+
+
 _LIB = None
 
 
@@ -143,6 +186,18 @@ def attention(args: AttnArgs, stream: int | None = None) -> None:
 def kernel_name(args: AttnArgs) -> str:
     lib = load()
     name = lib.sa_attention_kernel_name(ctypes.byref(args))
+    if name is None:
+        raise SaError(-1, lib.sa_last_error().decode())
+    return name.decode()
+
+
+def linear(args: LinearArgs, stream: int | None = None) -> None:
+    check(load().sa_linear_f32(ctypes.byref(args), stream))
+
+
+def linear_kernel_name(args: LinearArgs) -> str:
+    lib = load()
+    name = lib.sa_linear_kernel_name(ctypes.byref(args))
     if name is None:
         raise SaError(-1, lib.sa_last_error().decode())
     return name.decode()

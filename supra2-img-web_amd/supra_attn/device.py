@@ -108,3 +108,6 @@ class Device:
 
     def attention(self, args: _lib.AttnArgs) -> None:
         _lib.attention(args, self.stream)
+
+    def linear(self, args: _lib.LinearArgs) -> None:
+        _lib.linear(args, self.stream)

@@ -67,3 +67,49 @@ class Staged:
         for b in self.bufs:
             b.release()
         self.bufs = []
+
+
+class StagedLinear:
+    """Device-resident buffers of one linear call plus its ready-to-launch sa_linear_args."""
+
+    def __init__(self, dev: Device, call):
+        self.dev = dev
+        self.call = call
+        self.bufs = []
+        x = self._put(call.x)
+        w = self._put(call.w)
+        self.y = self._put(call.y0)
+        kw = dict(M=call.M, N=call.N, K=call.K, x=x.ptr, x_off=call.x_off, ldx=call.ldx, w=w.ptr, ldw=call.ldw,
+                  alpha=call.alpha, act=call.act, epilogue=call.epi, y=self.y.ptr, y_off=call.y_off, ldy=call.ldy,
+                  gate_off=call.gate_off)
+        if call.bias is not None:
+            kw["bias"] = self._put(call.bias).ptr
+        if call.gate is not None:
+            kw["gate"] = self._put(call.gate).ptr
+        self.args = _lib.LinearArgs(**kw)
+
+    def _put(self, arr):
+        buf = self.dev.from_array(np.ascontiguousarray(arr))
+        self.bufs.append(buf)
+        return buf
+
+    def reset(self) -> None:
+        """Restore the initial output (the residual epilogues accumulate into it)."""
+        self.y.upload(self.call.y0)
+
+    def launch(self) -> None:
+        self.dev.linear(self.args)
+
+    def run(self) -> np.ndarray:
+        self.launch()
+        self.dev.sync()
+        return self.y.read()
+
+    @property
+    def kernel(self) -> str:
+        return _lib.linear_kernel_name(self.args)
+
+    def release(self) -> None:
+        for b in self.bufs:
+            b.release()
+        self.bufs = []

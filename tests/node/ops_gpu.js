@@ -77,6 +77,27 @@ var forms = {
     q.release();
     return out;
   },
+  // app/gpu/ops.js:35-43 linear() in the DiT block forms (dit.js:167, 175, 191): W uploaded as
+  // app/weights.js:89-101 does, gated or plain residual into an existing output
+  linear: function (gpu, c) {
+    var x = gpu.fromArray(loadBin(c.x), [c.M, c.K]);
+    var W = { kind: "f32", N: c.N, K: c.K, buf: gpu.upload(loadBin(c.w)), bias: c.bias ? gpu.upload(loadBin(c.bias)) : null };
+    var opts = { act: c.act };
+    if (c.resid) {
+      opts.out = gpu.fromArray(loadBin(c.y0), [c.M, c.N]);
+      opts.resid = true;
+    }
+    if (c.gate) {
+      opts.gate = gpu.fromArray(loadBin(c.gate), [c.gateLen]);
+      opts.gOff = c.gOff;
+    }
+    var y = sa.linear(gpu, x, W, opts);
+    x.release();
+    if (opts.gate) opts.gate.release();
+    gpu.native.free(W.buf);
+    if (W.bias) gpu.native.free(W.bias);
+    return y;
+  },
   // app/models/t5.js:73-80: dense [H, L, L] position bias, scale 1 (bias built on the device)
   t5_dense: function (gpu, c) {
     var q = gpu.fromArray(loadBin(c.q), [c.L, 768]);

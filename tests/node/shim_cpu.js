@@ -22,7 +22,7 @@ function check(name, fn) {
 }
 
 check("addon exports", function () {
-  ["attention", "kernelName", "workspaceBytes", "version", "deviceCount", "malloc", "free", "upload", "download", "memset", "copy", "sync",
+  ["attention", "kernelName", "workspaceBytes", "version", "deviceCount", "malloc", "free", "upload", "download", "memset", "copy", "sync", "linear", "linearKernelName",
     "bucketLut", "positionBias", "eventCreate", "eventRecord", "eventElapsed", "eventDestroy"].forEach(function (f) {
     assert.strictEqual(typeof native[f], "function", f);
   });
@@ -74,6 +74,8 @@ function fakeNative() {
     download: function () {},
     sync: function () {},
     attention: function (a) { this.calls.push(a); },
+    lin: [],
+    linear: function (a) { this.lin.push(a); },
     kernelName: function () { return "fake"; },
     wsBytes: 0,
     frees: 0,
@@ -223,6 +225,47 @@ check("batched DiT call sites: one launch per block (dit.js:169-173, 180-185)", 
   ctx.release();
   assert.strictEqual(ctx.kv.buf, null);
   assert.throws(function () { sa.dit.packContexts(g.gpu, kvs, [1, 2]); }, RangeError);
+});
+
+check("linear forms of the DiT block (dit.js:167, 175, 191; ops.js:35-43)", function () {
+  var g = makeGpu();
+  var R = 512, D = 576;
+  var h = g.gpu.empty([R, D]);
+  var Wqkv = { kind: "f32", N: 3 * D, K: D, buf: g.gpu.upload(new Float32Array(16)), bias: g.gpu.upload(new Float32Array(4)) };
+  var qkv = sa.linear(g.gpu, h, Wqkv);
+  assert.deepStrictEqual(qkv.shape, [R, 3 * D]);
+  var a = g.f.lin[0];
+  assert.strictEqual(a.M, R);
+  assert.strictEqual(a.N, 3 * D);
+  assert.strictEqual(a.K, D);
+  assert.strictEqual(a.w, Wqkv.buf);
+  assert.strictEqual(a.bias, Wqkv.bias);
+  assert.strictEqual(a.act, 0);
+  assert.strictEqual(a.epilogue, 0);
+  assert.strictEqual(a.y, qkv.buf);
+  // proj: out += gate[gOff + n] * (a W^T + b)
+  var x = g.gpu.empty([R, D]);
+  var mod = g.gpu.empty([1, 14 * 6 * D]);
+  var Wp = { kind: "f32", N: D, K: D, buf: g.gpu.upload(new Float32Array(16)), bias: null };
+  var ret = sa.linear(g.gpu, h, Wp, { out: x, resid: true, gate: mod, gOff: 2 * D });
+  assert.strictEqual(ret, x);
+  a = g.f.lin[1];
+  assert.strictEqual(a.epilogue, 2);
+  assert.strictEqual(a.gate, mod.buf);
+  assert.strictEqual(a.gateOff, 2 * D);
+  assert.strictEqual(a.bias, null);
+  // fc1 with GELU (tanh), cproj residual without a gate, rows/aOff
+  sa.linear(g.gpu, h, Wp, { act: "gelu_tanh" });
+  assert.strictEqual(g.f.lin[2].act, 2);
+  sa.linear(g.gpu, h, Wp, { out: x, resid: true });
+  assert.strictEqual(g.f.lin[3].epilogue, 1);
+  sa.linear(g.gpu, h, Wp, { rows: 100, aOff: 7 * D });
+  assert.strictEqual(g.f.lin[4].M, 100);
+  assert.strictEqual(g.f.lin[4].xOff, 7 * D);
+  assert.throws(function () { sa.linear(g.gpu, h, Wp, { act: "relu6" }); }, /unknown act/);
+  assert.throws(function () { sa.linear(g.gpu, h, { kind: "q8", N: D, K: D, buf: Wp.buf }); }, /f32/);
+  h.release();
+  assert.throws(function () { sa.linear(g.gpu, h, Wp); }, /released/);
 });
 
 check("released tensors are reused and cannot be passed again", function () {

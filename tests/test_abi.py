@@ -17,11 +17,12 @@ from supra_attn import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "supra_attn.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in sorted(os.listdir(os.path.join(ROOT, "include"))) if h.endswith(".h")]
 FAKE = 0x7F0000000000  # a device-looking address; validation only compares addresses
 
 
 def header_functions() -> list[str]:
-    text = open(HEADER).read()
+    text = "\n".join(open(h).read() for h in HEADERS)
     return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\**\s*(sa_\w+)\s*\(", text, flags=re.M)))
 
 
@@ -41,24 +42,29 @@ def test_version_and_constants():
     lib = _lib.load()
     assert lib.sa_version() == 2
     text = open(HEADER).read()
+    text += open(os.path.join(ROOT, "include", "supra_linear.h")).read()
     for name in ("SA_OK", "SA_ERR_INVALID", "SA_ERR_UNSUPPORTED", "SA_ERR_HIP", "SA_ERR_ALIAS", "SA_BIAS_NONE",
-                 "SA_BIAS_DENSE", "SA_BIAS_RELPOS", "SA_MASK_NONE", "SA_MASK_KEY_LEN", "SA_MASK_KEY_MASK"):
+                 "SA_BIAS_DENSE", "SA_BIAS_RELPOS", "SA_MASK_NONE", "SA_MASK_KEY_LEN", "SA_MASK_KEY_MASK",
+                 "SA_ACT_NONE", "SA_ACT_GELU", "SA_ACT_GELU_TANH", "SA_ACT_SILU", "SA_EPI_STORE", "SA_EPI_RESID",
+                 "SA_EPI_RESID_GATE"):
         m = re.search(rf"#define {name} \(?(-?\d+)\)?", text)
         assert m and int(m.group(1)) == getattr(_lib, name), name
 
 
-def test_struct_layout_matches_c(tmp_path):
-    fields = [f[0] for f in _lib.AttnArgs._fields_]
+@pytest.mark.parametrize("cls,ctype,header", [(_lib.AttnArgs, "sa_attn_args", "supra_attn.h"),
+                                              (_lib.LinearArgs, "sa_linear_args", "supra_linear.h")])
+def test_struct_layout_matches_c(tmp_path, cls, ctype, header):
+    fields = [f[0] for f in cls._fields_]
     src = tmp_path / "layout.c"
-    body = "\n".join(f'  printf("{f} %zu\\n", offsetof(sa_attn_args, {f}));' for f in fields)
-    src.write_text(f'#include <stdio.h>\n#include <stddef.h>\n#include "supra_attn.h"\nint main(void) {{\n'
-                   f'  printf("sizeof %zu\\n", sizeof(sa_attn_args));\n{body}\n  return 0;\n}}\n')
+    body = "\n".join(f'  printf("{f} %zu\\n", offsetof({ctype}, {f}));' for f in fields)
+    src.write_text(f'#include <stdio.h>\n#include <stddef.h>\n#include "{header}"\nint main(void) {{\n'
+                   f'  printf("sizeof %zu\\n", sizeof({ctype}));\n{body}\n  return 0;\n}}\n')
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-std=c11", f"-I{os.path.dirname(HEADER)}", str(src), "-o", str(exe)], check=True)
     lines = dict(ln.split() for ln in subprocess.run([str(exe)], capture_output=True, text=True).stdout.splitlines())
-    assert int(lines["sizeof"]) == ctypes.sizeof(_lib.AttnArgs)
+    assert int(lines["sizeof"]) == ctypes.sizeof(cls)
     for f in fields:
-        assert int(lines[f]) == getattr(_lib.AttnArgs, f).offset, f
+        assert int(lines[f]) == getattr(cls, f).offset, f
 
 
 def good_args(**over):
@@ -206,3 +212,52 @@ def test_workspace_is_checked_before_launch(over, code, text):
     over = {k: (need - 1 if v == "need-1" else need if v == "need" else v) for k, v in over.items()}
     assert rc_of(vae_args(**over)) == code
     assert text in _lib.load().sa_last_error().decode()
+
+
+def lin_args(**over):
+    M, N, K = over.pop("M", 512), over.pop("N", 1728), over.pop("K", 576)
+    kw = dict(M=M, N=N, K=K, x=FAKE, w=FAKE + (1 << 30), y=FAKE + (2 << 30), bias=FAKE + (3 << 30))
+    kw.update(over)
+    return _lib.LinearArgs(**kw)
+
+
+def test_linear_kernel_choice():
+    # DiT layers at batch 64 (16384 rows): 128 x 192 tiles for wide outputs, 128 x 64 for 576-wide ones
+    assert _lib.linear_kernel_name(lin_args(M=16384, N=1728, K=576)) == "linear_mfma_128x192"
+    assert _lib.linear_kernel_name(lin_args(M=16384, N=2304, K=576)) == "linear_mfma_128x192"
+    assert _lib.linear_kernel_name(lin_args(M=16384, N=576, K=576)) == "linear_mfma_128x64"
+    assert _lib.linear_kernel_name(lin_args(M=16384, N=576, K=2304)) == "linear_mfma_128x64"
+    assert _lib.linear_kernel_name(lin_args(M=77, N=1152, K=576)) == "linear_mfma_128x64"  # 6 wide tiles < CUs
+    assert _lib.linear_kernel_name(lin_args(K=36)) == "linear_generic"            # K % 8 != 0
+    assert _lib.linear_kernel_name(lin_args(x_off=1)) == "linear_generic"         # unaligned rows
+    assert _lib.linear_kernel_name(lin_args(x=FAKE + 4)) == "linear_generic"
+    assert _lib.linear_kernel_name(lin_args(ldw=578)) == "linear_generic"
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(struct_size=8), _lib.SA_ERR_INVALID),
+    (dict(M=0), _lib.SA_ERR_INVALID),
+    (dict(N=-1), _lib.SA_ERR_INVALID),
+    (dict(K=0), _lib.SA_ERR_INVALID),
+    (dict(x=0), _lib.SA_ERR_INVALID),
+    (dict(y=0), _lib.SA_ERR_INVALID),
+    (dict(ldx=100), _lib.SA_ERR_INVALID),
+    (dict(ldw=100), _lib.SA_ERR_INVALID),
+    (dict(ldy=100), _lib.SA_ERR_INVALID),
+    (dict(x_off=-4), _lib.SA_ERR_INVALID),
+    (dict(alpha=float("nan")), _lib.SA_ERR_INVALID),
+    (dict(act=9), _lib.SA_ERR_INVALID),
+    (dict(epilogue=3), _lib.SA_ERR_INVALID),
+    (dict(epilogue=2), _lib.SA_ERR_INVALID),                       # gated residual without a gate
+    (dict(y=FAKE + 4096), _lib.SA_ERR_ALIAS),                      # y inside x
+    (dict(y=FAKE + (1 << 30) + 64), _lib.SA_ERR_ALIAS),            # y inside w
+    (dict(bias=FAKE + (2 << 30) + 128), _lib.SA_ERR_ALIAS),        # bias inside y
+    (dict(epilogue=2, gate=FAKE + (2 << 30), gate_off=8), _lib.SA_ERR_ALIAS),
+])
+def test_invalid_linear_calls_are_rejected(over, code):
+    args = lin_args(**over)
+    if "struct_size" in over:
+        args.struct_size = over["struct_size"]
+    assert _lib.load().sa_linear_f32(ctypes.byref(args), None) == code
+    assert _lib.load().sa_last_error().decode()
+    assert _lib.load().sa_linear_kernel_name(ctypes.byref(args)) is None

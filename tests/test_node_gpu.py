@@ -71,6 +71,24 @@ def test_reference_call_forms_through_node(tmp_path):
                   "k": _save(d, "vk.bin", vae.k), "v": _save(d, "vv.bin", vae.v)})
     refs["vae"] = orc.reference_torch(vae).reshape(1024, 512)
 
+    from oracle import linear as ol
+    from supra_attn.linear_workloads import dit_block_linears
+
+    lin_refs = {}
+    acts = {0: "none", 1: "gelu", 2: "gelu_tanh", 3: "silu"}
+    for call in [c for c in dit_block_linears(B=1) if c.name in ("qkv", "proj", "fc1", "cproj")]:
+        name = "linear_" + call.name
+        case = {"name": name, "form": "linear", "M": call.M, "N": call.N, "K": call.K, "act": acts[call.act],
+                "x": _save(d, name + "_x.bin", call.x), "w": _save(d, name + "_w.bin", call.w),
+                "bias": _save(d, name + "_b.bin", call.bias), "resid": call.epi != 0}
+        if call.epi != 0:
+            case["y0"] = _save(d, name + "_y0.bin", call.y0)
+        if call.gate is not None:
+            case.update(gate=_save(d, name + "_g.bin", call.gate), gateLen=int(call.gate.size), gOff=call.gate_off)
+        cases.append(case)
+        lin_refs[name] = ol.linear_torch_fp32(call.x, call.w, call.y0, **call.oracle_kwargs()).reshape(call.M, call.N)
+    refs.update(lin_refs)
+
     with open(os.path.join(d, "manifest.json"), "w") as f:
         json.dump({"cases": cases}, f)
     print("[node gpu] running", [c["name"] for c in cases], flush=True)
