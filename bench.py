@@ -198,6 +198,22 @@ def linear_block(dev, B: int = 64, reps: int = 20, cpu: bool = True) -> dict:
     return out
 
 
+def vae_block_timing(dev, calls: int = 200) -> dict:
+    """The SD-VAE mid-block attention as one call (app/models/vae.js:77-94) at a 32x32 latent."""
+    from supra_attn.linear_workloads import vae_block
+    from supra_attn.runner import StagedVae
+
+    call = vae_block()
+    st = StagedVae(dev, call, in_place=False)
+    ms = time_calls(dev, st.launch, calls, warmup=10)
+    st.release()
+    tf = call.flops() / (ms * 1e-3) / 1e12
+    return {"workload": f"VAE mid-block attention, {call.HW} pixels x {call.C} channels: GroupNorm, q|k|v, "
+                        "attention, output projection + residual in one call",
+            "us_per_call": round(ms * 1e3, 2), "tflops": round(tf, 2), "frac_peak": round(tf / PEAK_TFLOPS, 4),
+            "flops_per_call": call.flops()}
+
+
 COPY_BYTES = 256 << 20
 
 
@@ -209,7 +225,13 @@ def profile_run(workload: str, launches: int) -> int:
     from supra_attn.runner import Staged
 
     dev = Device(0)
-    if workload.startswith("linear_"):
+    if workload == "vae_block":
+        from supra_attn.linear_workloads import vae_block
+        from supra_attn.runner import StagedVae
+
+        call = vae_block()
+        st = StagedVae(dev, call)
+    elif workload.startswith("linear_"):
         from supra_attn.linear_workloads import dit_block_linears
         from supra_attn.runner import StagedLinear
 
@@ -344,6 +366,8 @@ def main() -> int:
         }
         st.release()
         log(f"{name}: {ms * 1e3:.2f} us/call, {tf:.2f} TFLOP/s via {per_config[name]['kernel']}")
+    vae = vae_block_timing(dev)
+    log(f"vae_block: {vae['us_per_call']:.2f} us/call, {vae['tflops']:.2f} TFLOP/s")
     for s, c in staged:
         s.release()
         c.release()
@@ -403,6 +427,7 @@ def main() -> int:
                        for k, v in per_config.items()},
         "callsite": callsite,
         "linear": linear,
+        "vae_block": vae,
         "cpu_baseline": None if cpu is None else {k: (round(v, 6) if isinstance(v, float) else v) for k, v in cpu.items()},
     }
     print(json.dumps(result))

@@ -16,6 +16,7 @@
 
 #include "supra_attn.h"
 #include "supra_linear.h"
+#include "supra_vae.h"
 #include "common.h"
 #include "kernels.h"
 
@@ -197,6 +198,19 @@ int resolve_linear(const sa_linear_args* a, sa::LinearParams* p) {
   return SA_OK;
 }
 
+// Workspace of the VAE block (byte offsets, 256-byte aligned parts): normalized image [HW, C],
+// q|k|v [HW, 3C], attention output [HW, C], GroupNorm chunk statistics, then the attention call's
+// own scratch.
+struct VaeLayout {
+  int64_t n, qkv, a, gn, attn, total;
+};
+
+int64_t align256(int64_t b) { return (b + 255) & ~(int64_t)255; }
+
+// Sizes -> layout and the attention call over the q|k|v part of `ws` (any 256-byte aligned base
+// gives the same kernel choice as the real workspace, which is 16-byte aligned at least).
+int vae_plan(const sa_vae_attn_args* a, char* ws, VaeLayout* L, sa_attn_args* at);
+
 enum class Path { kFlash, kWide, kGeneric };
 
 struct Choice {
@@ -334,6 +348,82 @@ const char* sa_linear_kernel_name(const sa_linear_args* args) {
   if (resolve_linear(args, &p) != SA_OK) return nullptr;
   ok();
   return sa::linear_kernel_name(p, num_cus());
+}
+
+int sa_vae_attention_f32(const sa_vae_attn_args* a, void* stream) {
+  if (a == nullptr) return fail(SA_ERR_INVALID, "args is NULL");
+  VaeLayout L;
+  sa_attn_args at;
+  int rc = vae_plan(a, static_cast<char*>(a->workspace), &L, &at);
+  if (rc != SA_OK) return rc;
+  if (!a->x || !a->gamma || !a->beta || !a->wqkv || !a->wo || !a->out)
+    return fail(SA_ERR_INVALID, "x, gamma, beta, wqkv, wo and out must be non-NULL device pointers");
+  if (!a->workspace || a->workspace_bytes < L.total)
+    return fail(SA_ERR_INVALID, "this call needs a device workspace of %lld bytes (sa_vae_attention_workspace_bytes)",
+                (long long)L.total);
+  if (!aligned16(a->workspace)) return fail(SA_ERR_INVALID, "workspace must be 16-byte aligned");
+  const int64_t HW = a->HW, C = a->C;
+  auto span = [](const void* p, int64_t floats) -> Extent {
+    return {(uintptr_t)p, (uintptr_t)p + (uintptr_t)(floats * 4)};
+  };
+  const Extent ew = {(uintptr_t)a->workspace, (uintptr_t)a->workspace + (uintptr_t)L.total};
+  const Extent ex = span(a->x, HW * C), eo = span(a->out, HW * C);
+  if (overlaps(ew, ex) || overlaps(ew, eo)) return fail(SA_ERR_ALIAS, "the workspace overlaps x or out");
+  if (a->out != a->x && overlaps(eo, ex)) return fail(SA_ERR_ALIAS, "out overlaps x (pass out == x to update in place)");
+  const Extent params[] = {span(a->gamma, C), span(a->beta, C), span(a->wqkv, 3 * C * C),
+                           span(a->bqkv ? a->bqkv : a->gamma, a->bqkv ? 3 * C : 0), span(a->wo, C * C),
+                           span(a->bo ? a->bo : a->gamma, a->bo ? C : 0)};
+  for (const Extent& e : params)
+    if (overlaps(e, eo) || overlaps(e, ew)) return fail(SA_ERR_ALIAS, "out or the workspace overlaps a parameter");
+
+  char* ws = static_cast<char*>(a->workspace);
+  float* n = reinterpret_cast<float*>(ws + L.n);
+  float* qkv = reinterpret_cast<float*>(ws + L.qkv);
+  float* att = reinterpret_cast<float*>(ws + L.a);
+  sa_linear_args l1 = {};
+  l1.struct_size = sizeof l1;
+  l1.M = a->HW;
+  l1.N = 3 * a->C;
+  l1.K = a->C;
+  l1.x = n;
+  l1.w = a->wqkv;
+  l1.bias = a->bqkv;
+  l1.alpha = 1.f;
+  l1.y = qkv;
+  sa_linear_args l2 = l1;
+  l2.N = a->C;
+  l2.x = att;
+  l2.w = a->wo;
+  l2.bias = a->bo;
+  l2.epilogue = SA_EPI_RESID;
+  l2.y = a->out;
+  // every part is validated before the first launch, so a rejected call launches nothing
+  if (!sa_linear_kernel_name(&l1) || !sa_attention_kernel_name(&at) || !sa_linear_kernel_name(&l2)) {
+    char why[sizeof(g_err)];
+    memcpy(why, g_err, sizeof why);
+    return fail(SA_ERR_INVALID, "VAE block: %s", why);
+  }
+  const hipStream_t st = (hipStream_t)stream;
+  hipError_t e = sa::launch_groupnorm(a->x, a->gamma, a->beta, n, reinterpret_cast<float*>(ws + L.gn), a->HW, a->C,
+                                      a->groups, a->eps, st);
+  if (e != hipSuccess) return hip_fail(e, "groupnorm");
+  if ((rc = sa_linear_f32(&l1, stream)) != SA_OK) return rc;
+  if ((rc = sa_attention_f32(&at, stream)) != SA_OK) return rc;
+  if (a->out != a->x) {
+    e = hipMemcpyAsync(a->out, a->x, (size_t)(HW * C * 4), hipMemcpyDeviceToDevice, st);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync");
+  }
+  if ((rc = sa_linear_f32(&l2, stream)) != SA_OK) return rc;
+  return ok();
+}
+
+int64_t sa_vae_attention_workspace_bytes(const sa_vae_attn_args* a) {
+  VaeLayout L;
+  sa_attn_args at;
+  const int rc = vae_plan(a, reinterpret_cast<char*>((uintptr_t)1 << 40), &L, &at);
+  if (rc != SA_OK) return rc;
+  ok();
+  return L.total;
 }
 
 const char* sa_attention_kernel_name(const sa_attn_args* args) {
@@ -509,3 +599,48 @@ int sa_version(void) { return SA_ABI_VERSION; }
 const char* sa_last_error(void) { return g_err; }
 
 }  // extern "C"
+
+namespace {
+
+int vae_plan(const sa_vae_attn_args* a, char* ws, VaeLayout* L, sa_attn_args* at) {
+  if (a == nullptr) return fail(SA_ERR_INVALID, "args is NULL");
+  if (a->struct_size != sizeof(sa_vae_attn_args))
+    return fail(SA_ERR_INVALID, "struct_size %u does not match sizeof(sa_vae_attn_args) = %zu", a->struct_size,
+                sizeof(sa_vae_attn_args));
+  if (a->HW <= 0 || a->C <= 0 || a->groups <= 0)
+    return fail(SA_ERR_INVALID, "HW, C and groups must be positive (got %d, %d, %d)", a->HW, a->C, a->groups);
+  if (a->C % a->groups != 0) return fail(SA_ERR_INVALID, "C = %d is not a multiple of groups = %d", a->C, a->groups);
+  if (a->groups > 8192) return fail(SA_ERR_UNSUPPORTED, "at most 8192 GroupNorm groups");
+  if (!(a->eps >= 0.f) || !isfinite(a->eps)) return fail(SA_ERR_INVALID, "eps must be finite and >= 0");
+  if ((int64_t)a->C * 3 > 0x7fffffff) return fail(SA_ERR_UNSUPPORTED, "C too large");
+  if (ws == nullptr) ws = reinterpret_cast<char*>((uintptr_t)1 << 40);  // layout only; checked by the caller
+  const int64_t HW = a->HW, C = a->C;
+  L->n = 0;
+  L->qkv = align256(HW * C * 4);
+  L->a = L->qkv + align256(HW * 3 * C * 4);
+  L->gn = L->a + align256(HW * C * 4);
+  L->attn = L->gn + align256((int64_t)3 * a->groups * sa::groupnorm_chunks(a->HW, a->groups) * 4);
+  *at = sa_attn_args{};
+  at->struct_size = sizeof(sa_attn_args);
+  at->B = 1;
+  at->H = 1;
+  at->D = a->C;
+  at->Lq = a->HW;
+  at->Lk = a->HW;
+  float* qkv = reinterpret_cast<float*>(ws + L->qkv);
+  at->q = at->k = at->v = qkv;
+  at->k_off = C;
+  at->v_off = 2 * C;
+  at->ldq = at->ldk = at->ldv = 3 * C;
+  at->o = reinterpret_cast<float*>(ws + L->a);
+  at->ldo = C;
+  at->scale = 1.f / sqrtf((float)a->C);  // diffusers Attention default scale (vae.js:86: ops.js default)
+  const int64_t attn_bytes = sa_attention_workspace_bytes(at);
+  if (attn_bytes < 0) return (int)attn_bytes;
+  at->workspace = attn_bytes > 0 ? ws + L->attn : nullptr;
+  at->workspace_bytes = attn_bytes;
+  L->total = L->attn + align256(attn_bytes);
+  return SA_OK;
+}
+
+}  // namespace

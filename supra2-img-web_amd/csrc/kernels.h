@@ -86,4 +86,10 @@ LinearTile linear_mfma_tile(const LinearParams& p, int num_cus);
 const char* linear_kernel_name(const LinearParams& p, int num_cus);
 hipError_t launch_linear(const LinearParams& p, int num_cus, hipStream_t stream);
 
+// ---- GroupNorm over an NHWC image [HW, C] in `groups` channel groups (csrc/groupnorm.hip).
+// part: scratch of 3 * groups * groupnorm_chunks(HW, groups) floats for the chunk statistics.
+int groupnorm_chunks(int HW, int groups);
+hipError_t launch_groupnorm(const float* x, const float* gamma, const float* beta, float* y, float* part, int HW, int C,
+                            int groups, float eps, hipStream_t stream);
+
 }  // namespace sa

@@ -369,13 +369,16 @@ LinearTile linear_mfma_tile(const LinearParams& p, int num_cus) {
   // 404 vs 452). Narrow tiles also keep small-M calls spread over the CUs.
   const int64_t tiles_wide = ((p.M + 127) / 128) * ((p.N + 191) / 192);
   if (p.N >= 1024 && tiles_wide >= num_cus) return {2, 3};
+  // small calls (the 1024-row VAE projections): 64 x 64 tiles, so that more CUs get work
+  const int64_t tiles_narrow = ((p.M + 127) / 128) * ((p.N + 63) / 64);
+  if (tiles_narrow < 2 * num_cus) return {1, 1};
   return {2, 1};
 }
 
 const char* linear_kernel_name(const LinearParams& p, int num_cus) {
   if (!linear_mfma_supported(p)) return "linear_generic";
   const LinearTile t = linear_mfma_tile(p, num_cus);
-  return t.wn == 3 ? "linear_mfma_128x192" : "linear_mfma_128x64";
+  return t.wn == 3 ? "linear_mfma_128x192" : t.wm == 2 ? "linear_mfma_128x64" : "linear_mfma_64x64";
 }
 
 hipError_t launch_linear(const LinearParams& p, int num_cus, hipStream_t stream) {
@@ -387,7 +390,8 @@ hipError_t launch_linear(const LinearParams& p, int num_cus, hipStream_t stream)
   }
   const LinearTile t = linear_mfma_tile(p, num_cus);
   if (t.wn == 3) return launch_act<2, 3, 32, 2>(p, stream);
-  return launch_act<2, 1, 32, 2>(p, stream);
+  if (t.wm == 2) return launch_act<2, 1, 32, 2>(p, stream);
+  return launch_act<1, 1, 32, 2>(p, stream);
 }
 
 }  // namespace sa

@@ -20,6 +20,7 @@
 
 #include "supra_attn.h"
 #include "supra_linear.h"
+#include "supra_vae.h"
 
 static void* g_stream = NULL;
 static int g_stream_ready = 0;
@@ -271,6 +272,68 @@ static napi_value js_linear_kernel_name(napi_env env, napi_callback_info info) {
   }
   napi_value r;
   NAPI_CALL(env, napi_create_string_utf8(env, name, NAPI_AUTO_LENGTH, &r));
+  return r;
+}
+
+/* opts -> sa_vae_attn_args: HW, C, groups (32), eps (1e-6), x, gamma, beta, wqkv, bqkv, wo, bo,
+ * out, workspace, workspaceBytes. */
+static int fill_vae(napi_env env, napi_value o, sa_vae_attn_args* a) {
+  memset(a, 0, sizeof *a);
+  a->struct_size = sizeof *a;
+  int64_t HW, C, G;
+  double eps;
+  napi_value ev;
+  void *x, *gamma, *beta, *wqkv, *bqkv, *wo, *bo, *out, *ws;
+  if (prop_i64(env, o, "HW", -1, &HW) || prop_i64(env, o, "C", -1, &C) || prop_i64(env, o, "groups", 32, &G) ||
+      prop_i64(env, o, "workspaceBytes", 0, &a->workspace_bytes))
+    return 1;
+  if (prop(env, o, "eps", &ev) || get_f64(env, ev, 1e-6, &eps, "eps")) return 1;
+  if (prop_ptr(env, o, "x", &x) || prop_ptr(env, o, "gamma", &gamma) || prop_ptr(env, o, "beta", &beta) ||
+      prop_ptr(env, o, "wqkv", &wqkv) || prop_ptr(env, o, "bqkv", &bqkv) || prop_ptr(env, o, "wo", &wo) ||
+      prop_ptr(env, o, "bo", &bo) || prop_ptr(env, o, "out", &out) || prop_ptr(env, o, "workspace", &ws))
+    return 1;
+  if (HW > 0x7fffffffLL || C > 0x7fffffffLL || G > 0x7fffffffLL || HW < -1 || C < -1 || G < -1) {
+    napi_throw_range_error(env, "SA_ERR_INVALID", "sizes must fit in int32");
+    return 1;
+  }
+  a->HW = (int32_t)HW;
+  a->C = (int32_t)C;
+  a->groups = (int32_t)G;
+  a->eps = (float)eps;
+  a->x = (const float*)x;
+  a->gamma = (const float*)gamma;
+  a->beta = (const float*)beta;
+  a->wqkv = (const float*)wqkv;
+  a->bqkv = (const float*)bqkv;
+  a->wo = (const float*)wo;
+  a->bo = (const float*)bo;
+  a->out = (float*)out;
+  a->workspace = ws;
+  return 0;
+}
+
+static napi_value js_vae_attention(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (get_args(env, info, 1, argv)) return NULL;
+  sa_vae_attn_args a;
+  if (fill_vae(env, argv[0], &a)) return NULL;
+  if (ensure_stream(env)) return NULL;
+  if (throw_if(env, sa_vae_attention_f32(&a, g_stream))) return NULL;
+  return undefined(env);
+}
+
+static napi_value js_vae_workspace_bytes(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (get_args(env, info, 1, argv)) return NULL;
+  sa_vae_attn_args a;
+  if (fill_vae(env, argv[0], &a)) return NULL;
+  const int64_t n = sa_vae_attention_workspace_bytes(&a);
+  if (n < 0) {
+    throw_if(env, (int)n);
+    return NULL;
+  }
+  napi_value r;
+  NAPI_CALL(env, napi_create_double(env, (double)n, &r));
   return r;
 }
 
@@ -561,6 +624,8 @@ static napi_value init(napi_env env, napi_value exports) {
       {"kernelName", NULL, js_kernel_name, NULL, NULL, NULL, napi_enumerable, NULL},
       {"workspaceBytes", NULL, js_workspace_bytes, NULL, NULL, NULL, napi_enumerable, NULL},
       {"linear", NULL, js_linear, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"vaeAttention", NULL, js_vae_attention, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"vaeWorkspaceBytes", NULL, js_vae_workspace_bytes, NULL, NULL, NULL, napi_enumerable, NULL},
       {"linearKernelName", NULL, js_linear_kernel_name, NULL, NULL, NULL, napi_enumerable, NULL},
       {"version", NULL, js_version, NULL, NULL, NULL, napi_enumerable, NULL},
       {"deviceCount", NULL, js_device_count, NULL, NULL, NULL, napi_enumerable, NULL},

@@ -1,11 +1,12 @@
 // Entry point of the JS binding: the device runtime, the attention operator, the batched DiT call
-// sites and the linear layer either side of attention.
+// sites, the linear layer either side of attention and the VAE mid-block attention.
 "use strict";
 
 var device = require("./device");
 var ops = require("./ops");
 var dit = require("./dit_attn");
 var lin = require("./linear");
+var vae = require("./vae_attn");
 
 module.exports = {
   GPU: device.GPU,
@@ -19,4 +20,5 @@ module.exports = {
   dit: dit,
   linear: lin.linear,
   linearKernel: lin.linearKernel,
+  vae: vae,
 };

@@ -1,4 +1,4 @@
-"""ctypes binding of libsupra_attn.so (include/supra_attn.h, include/supra_linear.h).
+"""ctypes binding of libsupra_attn.so (include/supra_attn.h, supra_linear.h, supra_vae.h).
 
 Loading fails loudly when the library has not been built: there is no other implementation of the
 operator behind this module.
@@ -43,6 +43,8 @@ SIGNATURES = {
     "sa_attention_workspace_bytes": (c_int64, [c_void_p]),
     "sa_linear_f32": (c_int, [c_void_p, c_void_p]),
     "sa_linear_kernel_name": (c_char_p, [c_void_p]),
+    "sa_vae_attention_f32": (c_int, [c_void_p, c_void_p]),
+    "sa_vae_attention_workspace_bytes": (c_int64, [c_void_p]),
     "sa_t5_bucket_lut": (c_int, [c_int32, c_int32, c_int32, c_int32, c_int32, POINTER(c_int32)]),
     "sa_t5_position_bias": (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p]),
     "sa_device_count": (c_int, [POINTER(c_int32)]),
@@ -154,6 +156,36 @@ class LinearArgs(ctypes.Structure):
             setattr(self, name, val)
 
 
+class VaeAttnArgs(ctypes.Structure):
+    """Mirror of sa_vae_attn_args (include/supra_vae.h); groups default 32, eps 1e-6."""
+
+    _fields_ = [
+        ("struct_size", c_uint32),
+        ("HW", c_int32),
+        ("C", c_int32),
+        ("groups", c_int32),
+        ("eps", c_float),
+        ("x", c_void_p),
+        ("gamma", c_void_p),
+        ("beta", c_void_p),
+        ("wqkv", c_void_p),
+        ("bqkv", c_void_p),
+        ("wo", c_void_p),
+        ("bo", c_void_p),
+        ("out", c_void_p),
+        ("workspace", c_void_p),
+        ("workspace_bytes", c_int64),
+    ]
+
+    def __init__(self, **kw):
+        super().__init__()
+        self.struct_size = ctypes.sizeof(VaeAttnArgs)
+        self.groups = 32
+        self.eps = 1e-6
+        for name, val in kw.items():
+            setattr(self, name, val)
+
+
 _LIB = None
 
 
@@ -201,6 +233,18 @@ def linear_kernel_name(args: LinearArgs) -> str:
     if name is None:
         raise SaError(-1, lib.sa_last_error().decode())
     return name.decode()
+
+
+def vae_attention(args: VaeAttnArgs, stream: int | None = None) -> None:
+    check(load().sa_vae_attention_f32(ctypes.byref(args), stream))
+
+
+def vae_workspace_bytes(args: VaeAttnArgs) -> int:
+    lib = load()
+    n = lib.sa_vae_attention_workspace_bytes(ctypes.byref(args))
+    if n < 0:
+        raise SaError(int(n), lib.sa_last_error().decode())
+    return int(n)
 
 
 def workspace_bytes(args: AttnArgs) -> int:

@@ -12,6 +12,9 @@ The shapes and epilogues follow app/models/dit.js:165-192 with R = B*256 rows (d
 and the per-prompt context projection kv [L, 576] -> [L, 1152] (dit.js:141). Weights ~ N(0, 1/K)
 (unit-variance outputs), activations and the residual stream ~ N(0, 1), biases ~ N(0, 0.1^2),
 gates ~ N(0, 1). FLOPs count 2*M*N*K (app/gpu/ops.js:24).
+
+Also the SD-VAE mid-block attention as one call (`vae_block`, app/models/vae.js:77-94): GroupNorm,
+the q/k/v projections, one-head attention, the output projection and the residual.
 """
 
 from __future__ import annotations
@@ -97,3 +100,43 @@ def dit_block_linears(B: int = 64, seed: int = 20) -> list[LinearCall]:
 def context_kv(L: int = 77, seed: int = 26) -> LinearCall:
     """Per-prompt cross-attention keys/values of one block (dit.js:141): [L, 576] -> [L, 1152]."""
     return make_linear("ctx_kv", L, 2 * DIT_DIM, DIT_DIM, seed=seed)
+
+
+@dataclass
+class VaeBlockCall:
+    """Host buffers of one VAE mid-block attention call (fields as in sa_vae_attn_args)."""
+
+    name: str
+    HW: int
+    C: int
+    groups: int
+    eps: float
+    x: np.ndarray      # [HW, C]
+    gamma: np.ndarray  # [C]
+    beta: np.ndarray
+    wqkv: np.ndarray   # [3C, C]
+    bqkv: np.ndarray | None
+    wo: np.ndarray     # [C, C]
+    bo: np.ndarray | None
+
+    def flops(self) -> int:
+        """Projections 2*HW*C*(3C + C) plus attention 4*C*HW^2 (app/gpu/ops.js:24, 116)."""
+        return 2 * self.HW * self.C * 4 * self.C + 4 * self.C * self.HW * self.HW
+
+    def algorithmic_bytes(self) -> int:
+        """x read, out written, the weights and vectors read once."""
+        return 4 * (2 * self.HW * self.C + 4 * self.C * self.C + 6 * self.C)
+
+    def oracle_args(self) -> tuple:
+        return (self.x, self.gamma, self.beta, self.wqkv, self.bqkv, self.wo, self.bo)
+
+
+def vae_block(HW: int = 1024, C: int = 512, groups: int = 32, seed: int = 30, bias: bool = True) -> VaeBlockCall:
+    """The SD-VAE mid-block attention (app/models/vae.js:77-94) at a 32x32 latent: x ~ N(0, 1),
+    GroupNorm affine ~ (1 + 0.1 N, 0.1 N), projections ~ N(0, 1/C), biases ~ 0.1 N."""
+    rng = np.random.default_rng(seed)
+    f = lambda *shape, s=1.0: (rng.standard_normal(shape, dtype=np.float32) * np.float32(s)).astype(np.float32)
+    return VaeBlockCall(name=f"vae_block_{HW}x{C}", HW=HW, C=C, groups=groups, eps=1e-6, x=f(HW, C),
+                        gamma=(1 + f(C, s=0.1)).astype(np.float32), beta=f(C, s=0.1), wqkv=f(3 * C, C, s=C ** -0.5),
+                        bqkv=f(3 * C, s=0.1) if bias else None, wo=f(C, C, s=C ** -0.5),
+                        bo=f(C, s=0.1) if bias else None)

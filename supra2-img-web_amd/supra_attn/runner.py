@@ -113,3 +113,55 @@ class StagedLinear:
         for b in self.bufs:
             b.release()
         self.bufs = []
+
+
+class StagedVae:
+    """Device-resident buffers of one VAE mid-block attention call, its workspace and args."""
+
+    def __init__(self, dev: Device, call, in_place: bool = False):
+        self.dev = dev
+        self.call = call
+        self.bufs = []
+        put = self._put
+        self.x = put(call.x)
+        self.out = self.x if in_place else dev.empty(call.x.shape)
+        if not in_place:
+            self.bufs.append(self.out)
+        kw = dict(HW=call.HW, C=call.C, groups=call.groups, eps=call.eps, x=self.x.ptr, gamma=put(call.gamma).ptr,
+                  beta=put(call.beta).ptr, wqkv=put(call.wqkv).ptr, wo=put(call.wo).ptr, out=self.out.ptr)
+        if call.bqkv is not None:
+            kw["bqkv"] = put(call.bqkv).ptr
+        if call.bo is not None:
+            kw["bo"] = put(call.bo).ptr
+        self.args = _lib.VaeAttnArgs(**kw)
+        n = _lib.vae_workspace_bytes(self.args)
+        ws = dev.empty(((n + 3) // 4,))
+        self.bufs.append(ws)
+        self.args.workspace = ws.ptr
+        self.args.workspace_bytes = n
+
+    def _put(self, arr):
+        buf = self.dev.from_array(np.ascontiguousarray(arr))
+        self.bufs.append(buf)
+        return buf
+
+    @property
+    def kernel(self) -> str:
+        return "groupnorm + linear + attention + linear"
+
+    def reset(self) -> None:
+        """Restore x (an in-place call overwrites it)."""
+        self.x.upload(self.call.x)
+
+    def launch(self) -> None:
+        _lib.vae_attention(self.args, self.dev.stream)
+
+    def run(self) -> np.ndarray:
+        self.launch()
+        self.dev.sync()
+        return self.out.read()
+
+    def release(self) -> None:
+        for b in self.bufs:
+            b.release()
+        self.bufs = []

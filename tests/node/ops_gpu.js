@@ -98,6 +98,17 @@ var forms = {
     if (W.bias) gpu.native.free(W.bias);
     return y;
   },
+  // app/models/vae.js:77-94 as one call: the weights as app/weights.js uploads them
+  vae_block: function (gpu, c) {
+    var C = c.C;
+    var up = function (f) { return gpu.upload(loadBin(f)); };
+    var lin = function (w, b) { return { kind: "f32", N: C, K: C, buf: up(w), bias: up(b) }; };
+    var A = { norm: { g: up(c.gamma), b: up(c.beta) }, q: lin(c.wq, c.bq), k: lin(c.wk, c.bk), v: lin(c.wv, c.bv), o: lin(c.wo, c.bo) };
+    var x = gpu.fromArray(loadBin(c.x), [c.HW, C]);
+    var y = sa.vae.attention(gpu, x, c.HW, A);
+    sa.vae.releaseWeights(gpu, A);
+    return y;
+  },
   // app/models/t5.js:73-80: dense [H, L, L] position bias, scale 1 (bias built on the device)
   t5_dense: function (gpu, c) {
     var q = gpu.fromArray(loadBin(c.q), [c.L, 768]);

@@ -22,7 +22,7 @@ function check(name, fn) {
 }
 
 check("addon exports", function () {
-  ["attention", "kernelName", "workspaceBytes", "version", "deviceCount", "malloc", "free", "upload", "download", "memset", "copy", "sync", "linear", "linearKernelName",
+  ["attention", "kernelName", "workspaceBytes", "version", "deviceCount", "malloc", "free", "upload", "download", "memset", "copy", "sync", "linear", "linearKernelName", "vaeAttention", "vaeWorkspaceBytes",
     "bucketLut", "positionBias", "eventCreate", "eventRecord", "eventElapsed", "eventDestroy"].forEach(function (f) {
     assert.strictEqual(typeof native[f], "function", f);
   });
@@ -76,6 +76,9 @@ function fakeNative() {
     attention: function (a) { this.calls.push(a); },
     lin: [],
     linear: function (a) { this.lin.push(a); },
+    vae: [],
+    vaeAttention: function (a) { this.vae.push(a); },
+    vaeWorkspaceBytes: function () { return 27328512; },
     kernelName: function () { return "fake"; },
     wsBytes: 0,
     frees: 0,
@@ -266,6 +269,32 @@ check("linear forms of the DiT block (dit.js:167, 175, 191; ops.js:35-43)", func
   assert.throws(function () { sa.linear(g.gpu, h, { kind: "q8", N: D, K: D, buf: Wp.buf }); }, /f32/);
   h.release();
   assert.throws(function () { sa.linear(g.gpu, h, Wp); }, /released/);
+});
+
+check("VAE mid-block attention (vae.js:77-94) as one call", function () {
+  var g = makeGpu();
+  var C = 512;
+  var lin = function () { return { kind: "f32", N: C, K: C, buf: g.gpu.upload(new Float32Array(4)), bias: g.gpu.upload(new Float32Array(4)) }; };
+  var A = { norm: { g: g.gpu.upload(new Float32Array(4)), b: g.gpu.upload(new Float32Array(4)) }, q: lin(), k: lin(), v: lin(), o: lin() };
+  var x = g.gpu.empty([1024, C]);
+  var ret = sa.vae.attention(g.gpu, x, 1024, A);
+  assert.strictEqual(ret, x);  // consumed and overwritten, as the reference's attention() consumes x
+  assert.strictEqual(g.f.copies.length, 6);  // q, k, v weights and biases packed once
+  var a = g.f.vae[0];
+  assert.strictEqual(a.HW, 1024);
+  assert.strictEqual(a.C, C);
+  assert.strictEqual(a.groups, 32);
+  assert.strictEqual(a.out, x.buf);
+  assert.strictEqual(a.x, x.buf);
+  assert.strictEqual(a.wo, A.o.buf);
+  assert.strictEqual(a.workspaceBytes, 27328512);
+  assert.deepStrictEqual(g.f.copies[2], [a.wqkv, C * C * 4, A.k.buf, 0, C * C * 4]);  // q.w, q.b, k.w, ...
+  assert.deepStrictEqual(g.f.copies[3], [a.bqkv, C * 4, A.k.bias, 0, C * 4]);
+  sa.vae.attention(g.gpu, x, 1024, A);
+  assert.strictEqual(g.f.copies.length, 6);  // cached
+  A.k.bias = null;
+  A._saQkv = null;
+  assert.throws(function () { sa.vae.attention(g.gpu, x, 1024, A); }, /biases or none/);
 });
 
 check("released tensors are reused and cannot be passed again", function () {

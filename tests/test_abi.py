@@ -52,7 +52,8 @@ def test_version_and_constants():
 
 
 @pytest.mark.parametrize("cls,ctype,header", [(_lib.AttnArgs, "sa_attn_args", "supra_attn.h"),
-                                              (_lib.LinearArgs, "sa_linear_args", "supra_linear.h")])
+                                              (_lib.LinearArgs, "sa_linear_args", "supra_linear.h"),
+                                              (_lib.VaeAttnArgs, "sa_vae_attn_args", "supra_vae.h")])
 def test_struct_layout_matches_c(tmp_path, cls, ctype, header):
     fields = [f[0] for f in cls._fields_]
     src = tmp_path / "layout.c"
@@ -227,7 +228,8 @@ def test_linear_kernel_choice():
     assert _lib.linear_kernel_name(lin_args(M=16384, N=2304, K=576)) == "linear_mfma_128x192"
     assert _lib.linear_kernel_name(lin_args(M=16384, N=576, K=576)) == "linear_mfma_128x64"
     assert _lib.linear_kernel_name(lin_args(M=16384, N=576, K=2304)) == "linear_mfma_128x64"
-    assert _lib.linear_kernel_name(lin_args(M=77, N=1152, K=576)) == "linear_mfma_128x64"  # 6 wide tiles < CUs
+    assert _lib.linear_kernel_name(lin_args(M=77, N=1152, K=576)) == "linear_mfma_64x64"  # small call: 64 x 64 tiles
+    assert _lib.linear_kernel_name(lin_args(M=1024, N=1536, K=512)) == "linear_mfma_64x64"  # VAE q|k|v
     assert _lib.linear_kernel_name(lin_args(K=36)) == "linear_generic"            # K % 8 != 0
     assert _lib.linear_kernel_name(lin_args(x_off=1)) == "linear_generic"         # unaligned rows
     assert _lib.linear_kernel_name(lin_args(x=FAKE + 4)) == "linear_generic"
@@ -261,3 +263,41 @@ def test_invalid_linear_calls_are_rejected(over, code):
     assert _lib.load().sa_linear_f32(ctypes.byref(args), None) == code
     assert _lib.load().sa_last_error().decode()
     assert _lib.load().sa_linear_kernel_name(ctypes.byref(args)) is None
+
+
+def vae_block_args(**over):
+    kw = dict(HW=1024, C=512, x=FAKE, gamma=FAKE + (1 << 30), beta=FAKE + (1 << 30) + 4096, wqkv=FAKE + (2 << 30),
+              wo=FAKE + (3 << 30), out=FAKE + (4 << 30), workspace=FAKE + (5 << 30))
+    kw["workspace_bytes"] = _lib.vae_workspace_bytes(_lib.VaeAttnArgs(**kw))
+    kw.update(over)
+    return _lib.VaeAttnArgs(**kw)
+
+
+def test_vae_workspace_size():
+    # normalized image + q|k|v + attention output (5 * HW * C floats) + the wide-head merge scratch
+    n = _lib.vae_workspace_bytes(vae_block_args())
+    assert n >= 5 * 1024 * 512 * 4 + _lib.workspace_bytes(_lib.AttnArgs(
+        B=1, H=1, D=512, Lq=1024, Lk=1024, q=FAKE, k=FAKE + 2048, v=FAKE + 4096, o=FAKE + (1 << 30),
+        ldq=1536, ldk=1536, ldv=1536, scale=0.044))
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(struct_size=8), _lib.SA_ERR_INVALID),
+    (dict(HW=0), _lib.SA_ERR_INVALID),
+    (dict(groups=0), _lib.SA_ERR_INVALID),
+    (dict(groups=7), _lib.SA_ERR_INVALID),                  # C % groups != 0
+    (dict(eps=float("nan")), _lib.SA_ERR_INVALID),
+    (dict(x=0), _lib.SA_ERR_INVALID),
+    (dict(workspace=0), _lib.SA_ERR_INVALID),
+    (dict(workspace_bytes=1024), _lib.SA_ERR_INVALID),
+    (dict(workspace=FAKE + (5 << 30) + 4), _lib.SA_ERR_INVALID),   # unaligned
+    (dict(out=FAKE + 64), _lib.SA_ERR_ALIAS),                      # partial overlap with x
+    (dict(out=FAKE + (2 << 30)), _lib.SA_ERR_ALIAS),               # out over the weights
+    (dict(workspace=FAKE + (4 << 30) + 1024), _lib.SA_ERR_ALIAS),  # workspace over out
+])
+def test_invalid_vae_calls_are_rejected(over, code):
+    args = vae_block_args(**over)
+    if "struct_size" in over:
+        args.struct_size = over["struct_size"]
+    assert _lib.load().sa_vae_attention_f32(ctypes.byref(args), None) == code
+    assert _lib.load().sa_last_error().decode()

@@ -29,4 +29,4 @@ def test_shim_and_addon_on_cpu(tmp_path):
     res = subprocess.run([NODE, os.path.join(ROOT, "tests", "node", "shim_cpu.js"), str(f)],
                          capture_output=True, text=True, timeout=120)
     assert res.returncode == 0, res.stdout + res.stderr
-    assert "all 10 checks passed" in res.stdout
+    assert "all 11 checks passed" in res.stdout

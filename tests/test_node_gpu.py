@@ -89,6 +89,20 @@ def test_reference_call_forms_through_node(tmp_path):
         lin_refs[name] = ol.linear_torch_fp32(call.x, call.w, call.y0, **call.oracle_kwargs()).reshape(call.M, call.N)
     refs.update(lin_refs)
 
+    from oracle import vae_block as ov
+    from supra_attn.linear_workloads import vae_block
+
+    vb = vae_block(seed=31)
+    C = vb.C
+    vcase = {"name": "vae_block", "form": "vae_block", "HW": vb.HW, "C": C, "x": _save(d, "vbx.bin", vb.x),
+             "gamma": _save(d, "vbg.bin", vb.gamma), "beta": _save(d, "vbb.bin", vb.beta),
+             "wo": _save(d, "vbwo.bin", vb.wo), "bo": _save(d, "vbbo.bin", vb.bo)}
+    for i, nm in enumerate("qkv"):
+        vcase["w" + nm] = _save(d, f"vbw{nm}.bin", vb.wqkv[i * C:(i + 1) * C])
+        vcase["b" + nm] = _save(d, f"vbb{nm}.bin", vb.bqkv[i * C:(i + 1) * C])
+    cases.append(vcase)
+    refs["vae_block"] = ov.block_torch_fp32(*vb.oracle_args())
+
     with open(os.path.join(d, "manifest.json"), "w") as f:
         json.dump({"cases": cases}, f)
     print("[node gpu] running", [c["name"] for c in cases], flush=True)
