@@ -363,22 +363,20 @@ bool linear_mfma_supported(const LinearParams& p) {
 }
 
 LinearTile linear_mfma_tile(const LinearParams& p, int num_cus) {
-  // Measured on the DiT layers at 16384 rows (after a warm-up, per layer): wide outputs run best
-  // on 128 x 192 tiles (qkv N = 1728: 282 us vs 286 for 128 x 64; fc1 N = 2304: 350 vs 371), the
-  // 576-wide ones on 128 x 64 tiles at three workgroups per CU (proj/q/cproj: 106 vs 120 us; fc2:
-  // 404 vs 452). Narrow tiles also keep small-M calls spread over the CUs.
+  // Measured on the DiT layers at 16384 rows (after a warm-up, per layer, eight tile / k-depth /
+  // stage variants): wide outputs run best on 128 x 192 tiles (qkv N = 1728: 283 us; fc1 N = 2304:
+  // 350 us; 128 x 64 tiles: 286 and 368), the 576-wide layers on 64 x 64 tiles at five workgroups per
+  // CU (proj/q/cproj 101 us, fc2 384 us; 128 x 64: 106 and 406). 64 x 64 tiles also spread small
+  // calls (the 1024-row VAE projections, per-prompt context projections) over more CUs.
   const int64_t tiles_wide = ((p.M + 127) / 128) * ((p.N + 191) / 192);
   if (p.N >= 1024 && tiles_wide >= num_cus) return {2, 3};
-  // small calls (the 1024-row VAE projections): 64 x 64 tiles, so that more CUs get work
-  const int64_t tiles_narrow = ((p.M + 127) / 128) * ((p.N + 63) / 64);
-  if (tiles_narrow < 2 * num_cus) return {1, 1};
-  return {2, 1};
+  return {1, 1};
 }
 
 const char* linear_kernel_name(const LinearParams& p, int num_cus) {
   if (!linear_mfma_supported(p)) return "linear_generic";
   const LinearTile t = linear_mfma_tile(p, num_cus);
-  return t.wn == 3 ? "linear_mfma_128x192" : t.wm == 2 ? "linear_mfma_128x64" : "linear_mfma_64x64";
+  return t.wn == 3 ? "linear_mfma_128x192" : "linear_mfma_64x64";
 }
 
 hipError_t launch_linear(const LinearParams& p, int num_cus, hipStream_t stream) {
@@ -390,7 +388,6 @@ hipError_t launch_linear(const LinearParams& p, int num_cus, hipStream_t stream)
   }
   const LinearTile t = linear_mfma_tile(p, num_cus);
   if (t.wn == 3) return launch_act<2, 3, 32, 2>(p, stream);
-  if (t.wm == 2) return launch_act<2, 1, 32, 2>(p, stream);
   return launch_act<1, 1, 32, 2>(p, stream);
 }
 
