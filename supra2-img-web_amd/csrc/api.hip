@@ -195,6 +195,9 @@ int resolve_linear(const sa_linear_args* a, sa::LinearParams* p) {
   p->alpha = a->alpha;
   p->act = a->act;
   p->epi = a->epilogue;
+  if (!sa::linear_mfma_supported(*p) && (int64_t)a->M > (int64_t)65535 * 16)  // generic kernel grid
+    return fail(SA_ERR_UNSUPPORTED, "M = %d exceeds the %d rows the unaligned / K %% 8 != 0 path supports", a->M,
+                65535 * 16);
   return SA_OK;
 }
 
@@ -371,10 +374,10 @@ int sa_vae_attention_f32(const sa_vae_attn_args* a, void* stream) {
   if (overlaps(ew, ex) || overlaps(ew, eo)) return fail(SA_ERR_ALIAS, "the workspace overlaps x or out");
   if (a->out != a->x && overlaps(eo, ex)) return fail(SA_ERR_ALIAS, "out overlaps x (pass out == x to update in place)");
   const Extent params[] = {span(a->gamma, C), span(a->beta, C), span(a->wqkv, 3 * C * C),
-                           span(a->bqkv ? a->bqkv : a->gamma, a->bqkv ? 3 * C : 0), span(a->wo, C * C),
-                           span(a->bo ? a->bo : a->gamma, a->bo ? C : 0)};
+                           span(a->bqkv, a->bqkv ? 3 * C : 0), span(a->wo, C * C), span(a->bo, a->bo ? C : 0)};
   for (const Extent& e : params)
-    if (overlaps(e, eo) || overlaps(e, ew)) return fail(SA_ERR_ALIAS, "out or the workspace overlaps a parameter");
+    if (e.lo != e.hi && (overlaps(e, eo) || overlaps(e, ew)))
+      return fail(SA_ERR_ALIAS, "out or the workspace overlaps a parameter");
 
   char* ws = static_cast<char*>(a->workspace);
   float* n = reinterpret_cast<float*>(ws + L.n);

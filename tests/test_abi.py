@@ -255,6 +255,7 @@ def test_linear_kernel_choice():
     (dict(y=FAKE + (1 << 30) + 64), _lib.SA_ERR_ALIAS),            # y inside w
     (dict(bias=FAKE + (2 << 30) + 128), _lib.SA_ERR_ALIAS),        # bias inside y
     (dict(epilogue=2, gate=FAKE + (2 << 30), gate_off=8), _lib.SA_ERR_ALIAS),
+    (dict(M=2000000, K=36, w=FAKE + (1 << 40), y=FAKE + (2 << 40), bias=0), _lib.SA_ERR_UNSUPPORTED),
 ])
 def test_invalid_linear_calls_are_rejected(over, code):
     args = lin_args(**over)
