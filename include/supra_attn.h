@@ -39,6 +39,9 @@ extern "C" {
 #define SA_ERR_UNSUPPORTED (-2) /* a valid request outside what this build implements */
 #define SA_ERR_HIP (-3)         /* the HIP runtime reported an error */
 #define SA_ERR_ALIAS (-4)       /* the output overlaps an input */
+#define SA_ERR_NOT_FOUND (-5)   /* a named tensor is not in the weight file (supra_weights.h) */
+#define SA_ERR_IO (-6)          /* a weight file could not be opened, sized or mapped */
+#define SA_ERR_FORMAT (-7)      /* a weight file is not well-formed safetensors */
 
 /* ---- additive score bias ---- */
 #define SA_BIAS_NONE 0
@@ -135,6 +138,8 @@ int sa_device_count(int32_t* count);
 int sa_set_device(int32_t device);
 int sa_malloc(void** ptr, size_t bytes);   /* device memory; synchronous */
 int sa_free(void* ptr);                    /* synchronous (waits for the device) */
+int sa_malloc_host(void** ptr, size_t bytes); /* pinned host memory (hipHostMalloc), e.g. sa_st_upload staging */
+int sa_free_host(void* ptr);               /* synchronous (waits for the device) */
 int sa_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream); /* returns when copied */
 int sa_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream); /* waits for stream */
 int sa_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream); /* stream-ordered */

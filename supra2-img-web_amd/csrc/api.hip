@@ -19,10 +19,13 @@
 #include "supra_vae.h"
 #include "common.h"
 #include "kernels.h"
+#include "status.h"
 
 namespace {
+thread_local char g_err[sa::kErrorBytes] = "";
+}  // namespace
 
-thread_local char g_err[512] = "";
+namespace sa {
 
 int fail(int code, const char* fmt, ...) {
   va_list ap;
@@ -40,6 +43,16 @@ int ok() {
 int hip_fail(hipError_t e, const char* what) {
   return fail(SA_ERR_HIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
 }
+
+const char* last_error() { return g_err; }
+
+}  // namespace sa
+
+namespace {
+
+using sa::fail;
+using sa::hip_fail;
+using sa::ok;
 
 // Byte extent [lo, hi) touched by a strided [B, L, H*D] view of `base`.
 struct Extent {
@@ -514,6 +527,19 @@ int sa_free(void* ptr) {
   if (!ptr) return ok();
   hipError_t e = hipFree(ptr);
   return e == hipSuccess ? ok() : hip_fail(e, "hipFree");
+}
+
+int sa_malloc_host(void** ptr, size_t bytes) {
+  if (!ptr) return fail(SA_ERR_INVALID, "ptr is NULL");
+  *ptr = nullptr;
+  hipError_t e = hipHostMalloc(ptr, bytes == 0 ? 16 : bytes, hipHostMallocDefault);
+  return e == hipSuccess ? ok() : hip_fail(e, "hipHostMalloc");
+}
+
+int sa_free_host(void* ptr) {
+  if (!ptr) return ok();
+  hipError_t e = hipHostFree(ptr);
+  return e == hipSuccess ? ok() : hip_fail(e, "hipHostFree");
 }
 
 int sa_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream) {

@@ -16,11 +16,13 @@
 
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "supra_attn.h"
 #include "supra_linear.h"
 #include "supra_vae.h"
+#include "supra_weights.h"
 
 static void* g_stream = NULL;
 static int g_stream_ready = 0;
@@ -45,6 +47,9 @@ static const char* status_code(int rc) {
     case SA_ERR_UNSUPPORTED: return "SA_ERR_UNSUPPORTED";
     case SA_ERR_HIP: return "SA_ERR_HIP";
     case SA_ERR_ALIAS: return "SA_ERR_ALIAS";
+    case SA_ERR_NOT_FOUND: return "SA_ERR_NOT_FOUND";
+    case SA_ERR_IO: return "SA_ERR_IO";
+    case SA_ERR_FORMAT: return "SA_ERR_FORMAT";
     default: return "SA_ERR";
   }
 }
@@ -618,6 +623,311 @@ static napi_value js_event_destroy(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
+/* ---- safetensors (include/supra_weights.h) ---- */
+
+/* The JS handle of an opened file: closed by stClose or, failing that, when collected. Bytes
+ * opened from a JS array are copied, so that the handle does not depend on the array's storage. */
+typedef struct StHandle {
+  sa_st_file* f;
+  void* copy;
+} StHandle;
+
+static void st_finalize(napi_env env, void* data, void* hint) {
+  (void)env;
+  (void)hint;
+  StHandle* h = (StHandle*)data;
+  if (h->f) sa_st_close(h->f);
+  free(h->copy);
+  free(h);
+}
+
+static napi_value st_wrap(napi_env env, sa_st_file* f, void* copy) {
+  StHandle* h = (StHandle*)calloc(1, sizeof *h);
+  if (!h) {
+    sa_st_close(f);
+    free(copy);
+    napi_throw_error(env, "SA_NAPI", "out of host memory");
+    return NULL;
+  }
+  h->f = f;
+  h->copy = copy;
+  napi_value r;
+  if (napi_create_external(env, h, st_finalize, NULL, &r) != napi_ok) {
+    st_finalize(env, h, NULL);
+    napi_throw_error(env, "SA_NAPI", "cannot create the file handle");
+    return NULL;
+  }
+  return r;
+}
+
+static int st_get(napi_env env, napi_value v, sa_st_file** out) {
+  void* p = NULL;
+  napi_valuetype t;
+  if (napi_typeof(env, v, &t) != napi_ok || t != napi_external || napi_get_value_external(env, v, &p) != napi_ok || !p) {
+    napi_throw_type_error(env, "SA_ERR_INVALID", "expected a safetensors handle");
+    return 1;
+  }
+  *out = ((StHandle*)p)->f;
+  if (!*out) {
+    napi_throw_error(env, "SA_ERR_INVALID", "the safetensors handle is closed");
+    return 1;
+  }
+  return 0;
+}
+
+static int get_string(napi_env env, napi_value v, char* buf, size_t cap, const char* what) {
+  size_t len = 0;
+  if (napi_get_value_string_utf8(env, v, buf, cap, &len) != napi_ok || len + 1 >= cap) {
+    char msg[128];
+    snprintf(msg, sizeof msg, "%s must be a string shorter than %zu bytes", what, cap - 1);
+    napi_throw_type_error(env, "SA_ERR_INVALID", msg);
+    return 1;
+  }
+  return 0;
+}
+
+static napi_value js_st_open(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (get_args(env, info, 1, argv)) return NULL;
+  char path[4096];
+  if (get_string(env, argv[0], path, sizeof path, "path")) return NULL;
+  sa_st_file* f = NULL;
+  if (throw_if(env, sa_st_open(path, &f))) return NULL;
+  return st_wrap(env, f, NULL);
+}
+
+static napi_value js_st_open_bytes(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (get_args(env, info, 1, argv)) return NULL;
+  void* data;
+  size_t bytes;
+  if (typed_bytes(env, argv[0], &data, &bytes)) return NULL;
+  void* copy = malloc(bytes ? bytes : 1);
+  if (!copy) {
+    napi_throw_error(env, "SA_NAPI", "out of host memory");
+    return NULL;
+  }
+  memcpy(copy, data, bytes);
+  sa_st_file* f = NULL;
+  if (throw_if(env, sa_st_open_memory(copy, (int64_t)bytes, &f))) {
+    free(copy);
+    return NULL;
+  }
+  return st_wrap(env, f, copy);
+}
+
+static napi_value js_st_close(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (get_args(env, info, 1, argv)) return NULL;
+  void* p = NULL;
+  napi_valuetype t;
+  if (napi_typeof(env, argv[0], &t) == napi_ok && t == napi_external && napi_get_value_external(env, argv[0], &p) == napi_ok &&
+      p) {
+    StHandle* h = (StHandle*)p;
+    if (h->f) sa_st_close(h->f);
+    h->f = NULL;
+    free(h->copy);
+    h->copy = NULL;
+  }
+  return undefined(env);
+}
+
+static napi_value js_st_names(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (get_args(env, info, 1, argv)) return NULL;
+  sa_st_file* f;
+  if (st_get(env, argv[0], &f)) return NULL;
+  const int64_t n = sa_st_count(f);
+  napi_value arr, s;
+  NAPI_CALL(env, napi_create_array_with_length(env, (size_t)n, &arr));
+  for (int64_t i = 0; i < n; ++i) {
+    NAPI_CALL(env, napi_create_string_utf8(env, sa_st_name(f, i), NAPI_AUTO_LENGTH, &s));
+    NAPI_CALL(env, napi_set_element(env, arr, (uint32_t)i, s));
+  }
+  return arr;
+}
+
+/* (handle, name) -> {dtype, shape, data_offsets, code} (the header entry, app/weights.js:60-64) */
+static napi_value js_st_info(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (get_args(env, info, 2, argv)) return NULL;
+  sa_st_file* f;
+  char name[4096];
+  if (st_get(env, argv[0], &f) || get_string(env, argv[1], name, sizeof name, "name")) return NULL;
+  sa_st_tensor t;
+  memset(&t, 0, sizeof t);
+  t.struct_size = sizeof t;
+  if (throw_if(env, sa_st_info(f, name, &t))) return NULL;
+  napi_value o, v, shape, offs;
+  NAPI_CALL(env, napi_create_object(env, &o));
+  NAPI_CALL(env, napi_create_string_utf8(env, t.dtype_name, NAPI_AUTO_LENGTH, &v));
+  NAPI_CALL(env, napi_set_named_property(env, o, "dtype", v));
+  NAPI_CALL(env, napi_create_array_with_length(env, (size_t)t.ndim, &shape));
+  for (int i = 0; i < t.ndim; ++i) {
+    NAPI_CALL(env, napi_create_double(env, (double)t.shape[i], &v));
+    NAPI_CALL(env, napi_set_element(env, shape, (uint32_t)i, v));
+  }
+  NAPI_CALL(env, napi_set_named_property(env, o, "shape", shape));
+  NAPI_CALL(env, napi_create_array_with_length(env, 2, &offs));
+  NAPI_CALL(env, napi_create_double(env, (double)t.begin, &v));
+  NAPI_CALL(env, napi_set_element(env, offs, 0, v));
+  NAPI_CALL(env, napi_create_double(env, (double)t.end, &v));
+  NAPI_CALL(env, napi_set_element(env, offs, 1, v));
+  NAPI_CALL(env, napi_set_named_property(env, o, "data_offsets", offs));
+  NAPI_CALL(env, napi_create_int32(env, t.dtype, &v));
+  NAPI_CALL(env, napi_set_named_property(env, o, "code", v));
+  NAPI_CALL(env, napi_create_double(env, (double)t.numel, &v));
+  NAPI_CALL(env, napi_set_named_property(env, o, "numel", v));
+  return o;
+}
+
+static napi_value js_st_has(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (get_args(env, info, 2, argv)) return NULL;
+  sa_st_file* f;
+  char name[4096];
+  if (st_get(env, argv[0], &f) || get_string(env, argv[1], name, sizeof name, "name")) return NULL;
+  sa_st_tensor t;
+  memset(&t, 0, sizeof t);
+  t.struct_size = sizeof t;
+  napi_value r;
+  NAPI_CALL(env, napi_get_boolean(env, sa_st_info(f, name, &t) == SA_OK, &r));
+  return r;
+}
+
+static napi_value js_st_metadata(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (get_args(env, info, 1, argv)) return NULL;
+  sa_st_file* f;
+  if (st_get(env, argv[0], &f)) return NULL;
+  napi_value o, v;
+  NAPI_CALL(env, napi_create_object(env, &o));
+  const int64_t n = sa_st_metadata_count(f);
+  for (int64_t i = 0; i < n; ++i) {
+    const char* k = sa_st_metadata_key(f, i);
+    NAPI_CALL(env, napi_create_string_utf8(env, sa_st_metadata_value(f, k), NAPI_AUTO_LENGTH, &v));
+    NAPI_CALL(env, napi_set_named_property(env, o, k, v));
+  }
+  return o;
+}
+
+static napi_value js_st_data_bytes(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (get_args(env, info, 1, argv)) return NULL;
+  sa_st_file* f;
+  if (st_get(env, argv[0], &f)) return NULL;
+  napi_value r;
+  NAPI_CALL(env, napi_create_double(env, (double)sa_st_data_bytes(f), &r));
+  return r;
+}
+
+/* (handle, begin, end, dst, dstByteOffset, staging|null, stagingBytes): returns when copied */
+static napi_value js_st_upload(napi_env env, napi_callback_info info) {
+  napi_value argv[7];
+  if (get_args(env, info, 7, argv)) return NULL;
+  sa_st_file* f;
+  int64_t begin, end, doff, sbytes;
+  void *dst, *staging;
+  if (st_get(env, argv[0], &f) || get_i64(env, argv[1], 0, &begin, "begin") || get_i64(env, argv[2], -1, &end, "end") ||
+      get_ptr(env, argv[3], &dst, "dst") || get_i64(env, argv[4], 0, &doff, "dstByteOffset") ||
+      get_ptr(env, argv[5], &staging, "staging") || get_i64(env, argv[6], 0, &sbytes, "stagingBytes"))
+    return NULL;
+  if (doff < 0) {
+    napi_throw_range_error(env, "SA_ERR_INVALID", "dstByteOffset must be >= 0");
+    return NULL;
+  }
+  if (ensure_stream(env)) return NULL;
+  if (throw_if(env, sa_st_upload(f, begin, end, dst ? (char*)dst + doff : NULL, staging, sbytes, g_stream))) return NULL;
+  return undefined(env);
+}
+
+static napi_value js_malloc_host(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (get_args(env, info, 1, argv)) return NULL;
+  int64_t bytes;
+  if (get_i64(env, argv[0], -1, &bytes, "bytes")) return NULL;
+  if (bytes < 0) {
+    napi_throw_range_error(env, "SA_ERR_INVALID", "bytes must be >= 0");
+    return NULL;
+  }
+  void* p = NULL;
+  if (throw_if(env, sa_malloc_host(&p, (size_t)bytes))) return NULL;
+  napi_value r;
+  NAPI_CALL(env, napi_create_external(env, p, NULL, NULL, &r));
+  return r;
+}
+
+static napi_value js_free_host(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (get_args(env, info, 1, argv)) return NULL;
+  void* p;
+  if (get_ptr(env, argv[0], &p, "buffer")) return NULL;
+  if (throw_if(env, sa_free_host(p))) return NULL;
+  return undefined(env);
+}
+
+/* (src, srcByteOffset, dtype, n, dst, dstByteOffset) */
+static napi_value js_to_f32(napi_env env, napi_callback_info info) {
+  napi_value argv[6];
+  if (get_args(env, info, 6, argv)) return NULL;
+  void *src, *dst;
+  int64_t soff, dtype, n, doff;
+  if (get_ptr(env, argv[0], &src, "src") || get_i64(env, argv[1], 0, &soff, "srcByteOffset") ||
+      get_i64(env, argv[2], -1, &dtype, "dtype") || get_i64(env, argv[3], -1, &n, "n") ||
+      get_ptr(env, argv[4], &dst, "dst") || get_i64(env, argv[5], 0, &doff, "dstByteOffset"))
+    return NULL;
+  if (!src || !dst || soff < 0 || doff < 0) {
+    napi_throw_error(env, "SA_ERR_INVALID", "toF32 needs two buffers and offsets >= 0");
+    return NULL;
+  }
+  if (ensure_stream(env)) return NULL;
+  if (throw_if(env, sa_to_f32((char*)src + soff, (int32_t)dtype, n, (float*)((char*)dst + doff), g_stream))) return NULL;
+  return undefined(env);
+}
+
+/* (table, tableByteOffset, dtype, rows, dim, ids, nIds, dst) */
+static napi_value js_rows_f32(napi_env env, napi_callback_info info) {
+  napi_value argv[8];
+  if (get_args(env, info, 8, argv)) return NULL;
+  void *table, *ids, *dst;
+  int64_t toff, dtype, rows, dim, n_ids;
+  if (get_ptr(env, argv[0], &table, "table") || get_i64(env, argv[1], 0, &toff, "tableByteOffset") ||
+      get_i64(env, argv[2], -1, &dtype, "dtype") || get_i64(env, argv[3], -1, &rows, "rows") ||
+      get_i64(env, argv[4], -1, &dim, "dim") || get_ptr(env, argv[5], &ids, "ids") ||
+      get_i64(env, argv[6], -1, &n_ids, "nIds") || get_ptr(env, argv[7], &dst, "dst"))
+    return NULL;
+  if (!table || toff < 0) {
+    napi_throw_error(env, "SA_ERR_INVALID", "rowsF32 needs a table and tableByteOffset >= 0");
+    return NULL;
+  }
+  if (ensure_stream(env)) return NULL;
+  if (throw_if(env, sa_rows_f32((char*)table + toff, (int32_t)dtype, rows, dim, (const int32_t*)ids, n_ids, (float*)dst,
+                                g_stream)))
+    return NULL;
+  return undefined(env);
+}
+
+/* (w, wByteOffset, dtype, cout, cin, cinPad, dst) */
+static napi_value js_conv3_pack(napi_env env, napi_callback_info info) {
+  napi_value argv[7];
+  if (get_args(env, info, 7, argv)) return NULL;
+  void *w, *dst;
+  int64_t woff, dtype, cout, cin, cp;
+  if (get_ptr(env, argv[0], &w, "w") || get_i64(env, argv[1], 0, &woff, "wByteOffset") ||
+      get_i64(env, argv[2], -1, &dtype, "dtype") || get_i64(env, argv[3], -1, &cout, "cout") ||
+      get_i64(env, argv[4], -1, &cin, "cin") || get_i64(env, argv[5], 0, &cp, "cinPad") || get_ptr(env, argv[6], &dst, "dst"))
+    return NULL;
+  if (!w || woff < 0 || cout > INT32_MAX || cin > INT32_MAX || cp > INT32_MAX) {
+    napi_throw_error(env, "SA_ERR_INVALID", "conv3Pack needs a weight buffer, wByteOffset >= 0 and 32-bit sizes");
+    return NULL;
+  }
+  if (ensure_stream(env)) return NULL;
+  if (throw_if(env, sa_conv3_pack_f32((char*)w + woff, (int32_t)dtype, (int32_t)cout, (int32_t)cin, (int32_t)cp,
+                                      (float*)dst, g_stream)))
+    return NULL;
+  return undefined(env);
+}
+
 static napi_value init(napi_env env, napi_value exports) {
   const napi_property_descriptor props[] = {
       {"attention", NULL, js_attention, NULL, NULL, NULL, napi_enumerable, NULL},
@@ -642,6 +952,20 @@ static napi_value init(napi_env env, napi_value exports) {
       {"eventRecord", NULL, js_event_record, NULL, NULL, NULL, napi_enumerable, NULL},
       {"eventElapsed", NULL, js_event_elapsed, NULL, NULL, NULL, napi_enumerable, NULL},
       {"eventDestroy", NULL, js_event_destroy, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"stOpen", NULL, js_st_open, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"stOpenBytes", NULL, js_st_open_bytes, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"stClose", NULL, js_st_close, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"stNames", NULL, js_st_names, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"stInfo", NULL, js_st_info, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"stHas", NULL, js_st_has, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"stMetadata", NULL, js_st_metadata, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"stDataBytes", NULL, js_st_data_bytes, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"stUpload", NULL, js_st_upload, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"mallocHost", NULL, js_malloc_host, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"freeHost", NULL, js_free_host, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"toF32", NULL, js_to_f32, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"rowsF32", NULL, js_rows_f32, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"conv3Pack", NULL, js_conv3_pack, NULL, NULL, NULL, napi_enumerable, NULL},
   };
   NAPI_CALL(env, napi_define_properties(env, exports, sizeof props / sizeof props[0], props));
   napi_value c;
@@ -654,6 +978,16 @@ static napi_value init(napi_env env, napi_value exports) {
   CONST("SA_MASK_NONE", SA_MASK_NONE)
   CONST("SA_MASK_KEY_LEN", SA_MASK_KEY_LEN)
   CONST("SA_MASK_KEY_MASK", SA_MASK_KEY_MASK)
+  CONST("SA_DT_F32", SA_DT_F32)
+  CONST("SA_DT_F16", SA_DT_F16)
+  CONST("SA_DT_BF16", SA_DT_BF16)
+  CONST("SA_DT_F64", SA_DT_F64)
+  CONST("SA_DT_I64", SA_DT_I64)
+  CONST("SA_DT_I32", SA_DT_I32)
+  CONST("SA_DT_I16", SA_DT_I16)
+  CONST("SA_DT_I8", SA_DT_I8)
+  CONST("SA_DT_U8", SA_DT_U8)
+  CONST("SA_DT_BOOL", SA_DT_BOOL)
 #undef CONST
   return exports;
 }

@@ -1,5 +1,6 @@
 // Entry point of the JS binding: the device runtime, the attention operator, the batched DiT call
-// sites, the linear layer either side of attention and the VAE mid-block attention.
+// sites, the linear layer either side of attention, the VAE mid-block attention and the
+// safetensors weight loader.
 "use strict";
 
 var device = require("./device");
@@ -7,6 +8,7 @@ var ops = require("./ops");
 var dit = require("./dit_attn");
 var lin = require("./linear");
 var vae = require("./vae_attn");
+var weights = require("./weights");
 
 module.exports = {
   GPU: device.GPU,
@@ -21,4 +23,5 @@ module.exports = {
   linear: lin.linear,
   linearKernel: lin.linearKernel,
   vae: vae,
+  weights: weights,
 };

@@ -18,6 +18,9 @@ SA_ERR_INVALID = -1
 SA_ERR_UNSUPPORTED = -2
 SA_ERR_HIP = -3
 SA_ERR_ALIAS = -4
+SA_ERR_NOT_FOUND = -5
+SA_ERR_IO = -6
+SA_ERR_FORMAT = -7
 
 SA_BIAS_NONE = 0
 SA_BIAS_DENSE = 1
@@ -36,7 +39,12 @@ SA_EPI_STORE = 0
 SA_EPI_RESID = 1
 SA_EPI_RESID_GATE = 2
 
-# Every symbol include/supra_attn.h declares, with (restype, argtypes).
+# safetensors dtypes (include/supra_weights.h)
+SA_DT = {"OTHER": 0, "F32": 1, "F16": 2, "BF16": 3, "F64": 4, "I64": 5, "I32": 6, "I16": 7, "I8": 8, "U8": 9,
+         "BOOL": 10, "U16": 11, "U32": 12, "U64": 13, "F8_E4M3": 14, "F8_E5M2": 15}
+SA_ST_MAX_DIMS = 8
+
+# Every symbol include/*.h declares, with (restype, argtypes).
 SIGNATURES = {
     "sa_attention_f32": (c_int, [c_void_p, c_void_p]),
     "sa_attention_kernel_name": (c_char_p, [c_void_p]),
@@ -63,6 +71,23 @@ SIGNATURES = {
     "sa_event_destroy": (c_int, [c_void_p]),
     "sa_event_record": (c_int, [c_void_p, c_void_p]),
     "sa_event_elapsed_ms": (c_int, [POINTER(c_float), c_void_p, c_void_p]),
+    "sa_malloc_host": (c_int, [POINTER(c_void_p), c_size_t]),
+    "sa_free_host": (c_int, [c_void_p]),
+    "sa_st_open": (c_int, [c_char_p, POINTER(c_void_p)]),
+    "sa_st_open_memory": (c_int, [c_void_p, c_int64, POINTER(c_void_p)]),
+    "sa_st_close": (c_int, [c_void_p]),
+    "sa_st_count": (c_int64, [c_void_p]),
+    "sa_st_name": (c_char_p, [c_void_p, c_int64]),
+    "sa_st_info": (c_int, [c_void_p, c_char_p, c_void_p]),
+    "sa_st_metadata_count": (c_int64, [c_void_p]),
+    "sa_st_metadata_key": (c_char_p, [c_void_p, c_int64]),
+    "sa_st_metadata_value": (c_char_p, [c_void_p, c_char_p]),
+    "sa_st_data_bytes": (c_int64, [c_void_p]),
+    "sa_st_data": (c_void_p, [c_void_p]),
+    "sa_st_upload": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_void_p]),
+    "sa_to_f32": (c_int, [c_void_p, c_int32, c_int64, c_void_p, c_void_p]),
+    "sa_rows_f32": (c_int, [c_void_p, c_int32, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_void_p]),
+    "sa_conv3_pack_f32": (c_int, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p]),
     "sa_version": (c_int, []),
     "sa_last_error": (c_char_p, []),
 }
@@ -184,6 +209,26 @@ class VaeAttnArgs(ctypes.Structure):
         self.eps = 1e-6
         for name, val in kw.items():
             setattr(self, name, val)
+
+
+class StTensor(ctypes.Structure):
+    """sa_st_tensor: one safetensors header entry."""
+
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("dtype", c_int32),
+        ("elem_bytes", c_int32),
+        ("ndim", c_int32),
+        ("shape", c_int64 * SA_ST_MAX_DIMS),
+        ("numel", c_int64),
+        ("begin", c_int64),
+        ("end", c_int64),
+        ("dtype_name", ctypes.c_char * 16),
+    ]
+
+    def __init__(self):
+        super().__init__()
+        self.struct_size = ctypes.sizeof(StTensor)
 
 
 _LIB = None

@@ -131,6 +131,62 @@ var forms = {
       scale: 1, relpos: rp, keyMask: km });
     return a;
   },
+  // app/models/dit.js:90 then dit.js:167: uploadLinear from a safetensors file feeding the linear layer
+  st_linear: function (gpu, c) {
+    return sa.weights.SafeTensors.open(c.file).then(function (st) {
+      return sa.weights.uploadLinear(gpu, st, c.base).then(function (W) {
+        var x = gpu.fromArray(loadBin(c.x), [c.M, W.K]);
+        var y = sa.linear(gpu, x, W, {});
+        x.release();
+        gpu.native.free(W.buf);
+        gpu.native.free(W.bias);
+        st.close();
+        return y;
+      });
+    });
+  },
+  // app/models/t5.js:72: embedding rows of the token ids, then gpu.fromArray
+  st_rows: function (gpu, c) {
+    return sa.weights.SafeTensors.open(c.file).then(function (st) {
+      return st.rows(c.table, c.ids).then(function (rows) {
+        st.close();
+        return gpu.fromArray(rows, [c.ids.length, rows.length / c.ids.length]);
+      });
+    });
+  },
+  // app/models/vae.js:29: uploadConv3(gpu, st, "decoder.conv_in.", CIN_PAD)
+  st_conv3: function (gpu, c) {
+    return sa.weights.SafeTensors.open(c.file).then(function (st) {
+      return sa.weights.uploadConv3(gpu, st, c.base, c.cinPad).then(function (W) {
+        var out = gpu.empty([W.N * W.K]);
+        gpu.native.copy(out.buf, 0, W.buf, 0, W.N * W.K * 4);
+        gpu.sync();
+        gpu.native.free(W.buf);
+        if (W.bias) gpu.native.free(W.bias);
+        st.close();
+        return out;
+      });
+    });
+  },
+  // app/models/dit.js:72, 78-80: st.f32(name) on the host (here an F16 tensor), opened from bytes
+  st_f32: function (gpu, c) {
+    return sa.weights.SafeTensors.open(fs.readFileSync(c.file)).then(function (st) {
+      return st.f32(c.tensor).then(function (a) {
+        st.close();
+        return gpu.fromArray(a);
+      });
+    });
+  },
+  // app/weights.js:28-37 on raw bytes: toF32(u8, "BF16") and bf16ToF32
+  st_to_f32: function (gpu, c) {
+    var u8 = new Uint8Array(loadBin(c.raw, Uint8Array));
+    var a = sa.weights.toF32(u8, c.dtype);
+    var b = sa.weights.bf16ToF32(u8);
+    for (var i = 0; i < a.length; i++) {
+      if (a[i] !== b[i] && !(a[i] !== a[i] && b[i] !== b[i])) throw new Error("bf16ToF32 != toF32 at " + i);
+    }
+    return gpu.fromArray(a);
+  },
   // app/models/vae.js:86: single head, D = C = 512, default scale
   vae: function (gpu, c) {
     var q = gpu.fromArray(loadBin(c.q), [c.L, 512]);
@@ -145,8 +201,11 @@ sa.GPU.create().then(function (gpu) {
   manifest.cases.forEach(function (c) {
     chain = chain.then(function () {
       process.stdout.write("[node case] " + c.name + "\n");
-      var out = forms[c.form](gpu, c);
-      return gpu.sync().then(function () {
+      var out;
+      return Promise.resolve(forms[c.form](gpu, c)).then(function (o) {
+        out = o;
+        return gpu.sync();
+      }).then(function () {
         return gpu.read(out);
       }).then(function (data) {
         saveBin(c.name + ".out.bin", data);

@@ -313,4 +313,68 @@ check("released tensors are reused and cannot be passed again", function () {
   assert.strictEqual(device.BufferPool.round(5000), 5120);
 });
 
-process.stdout.write("all " + checks + " checks passed\n");
+var pending = [];
+
+function checkAsync(name, fn) {
+  pending.push(function () {
+    return Promise.resolve(fn()).then(function () {
+      checks++;
+      process.stdout.write("ok " + name + "\n");
+    });
+  });
+}
+
+checkAsync("safetensors header and errors through the addon (app/weights.js:40-64), host only", function () {
+  var exp = JSON.parse(fs.readFileSync(process.argv[3], "utf8"));
+  var W = sa.weights;
+  return W.SafeTensors.open(exp.file).then(function (st) {
+    assert.deepStrictEqual(st.names(), Object.keys(exp.header));
+    Object.keys(exp.header).forEach(function (n) {
+      assert.ok(st.has(n), n);
+      assert.deepStrictEqual(st.info(n), exp.header[n]);
+    });
+    assert.deepStrictEqual(st.metadata, exp.metadata);
+    assert.deepStrictEqual(Object.keys(st.header), Object.keys(exp.header));
+    assert.strictEqual(st.has("nope"), false);
+    assert.throws(function () { st.info("nope"); }, function (e) {
+      return e.code === "SA_ERR_NOT_FOUND" && /missing tensor nope/.test(e.message);
+    });
+    // checks that precede any device work
+    assert.throws(function () { st._entry("u16"); }, function (e) {
+      return e.code === "SA_ERR_UNSUPPORTED" && /unsupported dtype U16/.test(e.message);
+    });
+    return W.uploadConv3(null, st, "blocks.0.mlp.0.", 0).then(function () { assert.fail("conv of a linear"); }, function (e) {
+      assert.ok(/expected a 3x3 conv/.test(e.message), e.message);
+      st.close();
+      assert.throws(function () { st.names(); }, /closed|safetensors handle/);
+    });
+  }).then(function () {
+    var bytes = fs.readFileSync(exp.file);
+    return W.SafeTensors.open(bytes).then(function (st) {
+      assert.deepStrictEqual(st.names(), Object.keys(exp.header));
+      st.close();
+    });
+  }).then(function () {
+    return W.SafeTensors.open(new Uint8Array([5, 0, 0])).then(function () { assert.fail("opened"); }, function (e) {
+      assert.strictEqual(e.code, "SA_ERR_FORMAT");
+    });
+  }).then(function () {
+    return W.SafeTensors.open(exp.file + ".missing").then(function () { assert.fail("opened"); }, function (e) {
+      assert.strictEqual(e.code, "SA_ERR_IO");
+    });
+  }).then(function () {
+    assert.throws(function () { W.toF32(new Uint8Array(4), "U32"); }, /unsupported dtype U32/);
+    assert.strictEqual(native.SA_DT_BF16, 3);
+    ["stOpen", "stOpenBytes", "stClose", "stNames", "stInfo", "stHas", "stMetadata", "stDataBytes", "stUpload",
+      "mallocHost", "freeHost", "toF32", "rowsF32", "conv3Pack"].forEach(function (f) {
+      assert.strictEqual(typeof native[f], "function", f);
+    });
+  });
+});
+
+pending.reduce(function (p, f) { return p.then(f); }, Promise.resolve()).then(function () {
+  process.stdout.write("all " + checks + " checks passed\n");
+}, function (e) {
+  process.stderr.write("check failed: " + (e && e.stack ? e.stack : e) + "\n");
+  process.exit(1);
+});

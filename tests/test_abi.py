@@ -43,7 +43,13 @@ def test_version_and_constants():
     assert lib.sa_version() == 2
     text = open(HEADER).read()
     text += open(os.path.join(ROOT, "include", "supra_linear.h")).read()
-    for name in ("SA_OK", "SA_ERR_INVALID", "SA_ERR_UNSUPPORTED", "SA_ERR_HIP", "SA_ERR_ALIAS", "SA_BIAS_NONE",
+    weights = open(os.path.join(ROOT, "include", "supra_weights.h")).read()
+    for dt, code in _lib.SA_DT.items():
+        m = re.search(rf"#define SA_DT_{dt} (\d+)", weights)
+        assert m and int(m.group(1)) == code, dt
+    assert re.search(rf"#define SA_ST_MAX_DIMS {_lib.SA_ST_MAX_DIMS}\b", weights)
+    for name in ("SA_OK", "SA_ERR_INVALID", "SA_ERR_UNSUPPORTED", "SA_ERR_HIP", "SA_ERR_ALIAS", "SA_ERR_NOT_FOUND",
+                 "SA_ERR_IO", "SA_ERR_FORMAT", "SA_BIAS_NONE",
                  "SA_BIAS_DENSE", "SA_BIAS_RELPOS", "SA_MASK_NONE", "SA_MASK_KEY_LEN", "SA_MASK_KEY_MASK",
                  "SA_ACT_NONE", "SA_ACT_GELU", "SA_ACT_GELU_TANH", "SA_ACT_SILU", "SA_EPI_STORE", "SA_EPI_RESID",
                  "SA_EPI_RESID_GATE"):
@@ -53,7 +59,8 @@ def test_version_and_constants():
 
 @pytest.mark.parametrize("cls,ctype,header", [(_lib.AttnArgs, "sa_attn_args", "supra_attn.h"),
                                               (_lib.LinearArgs, "sa_linear_args", "supra_linear.h"),
-                                              (_lib.VaeAttnArgs, "sa_vae_attn_args", "supra_vae.h")])
+                                              (_lib.VaeAttnArgs, "sa_vae_attn_args", "supra_vae.h"),
+                                              (_lib.StTensor, "sa_st_tensor", "supra_weights.h")])
 def test_struct_layout_matches_c(tmp_path, cls, ctype, header):
     fields = [f[0] for f in cls._fields_]
     src = tmp_path / "layout.c"

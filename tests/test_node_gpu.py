@@ -103,6 +103,42 @@ def test_reference_call_forms_through_node(tmp_path):
     cases.append(vcase)
     refs["vae_block"] = ov.block_torch_fp32(*vb.oracle_args())
 
+    # the safetensors loader (app/weights.js) as the model loaders call it
+    from oracle import weights as ow
+    from safetensors.numpy import save_file
+
+    rng = np.random.default_rng(40)
+    st_path = os.path.join(d, "model.safetensors")
+    save_file({"blocks.0.self_attn.qkv.weight": (rng.standard_normal((1728, 576)) / 24).astype(np.float32),
+               "blocks.0.self_attn.qkv.bias": (rng.standard_normal(1728) * 0.1).astype(np.float32),
+               "blocks.0.mlp.0.weight": (rng.standard_normal((2304, 576)) / 24).astype(np.float16),
+               "shared.weight": rng.standard_normal((3000, 768)).astype(np.float32),
+               "decoder.conv_in.weight": rng.standard_normal((512, 4, 3, 3)).astype(np.float32),
+               "decoder.conv_in.bias": rng.standard_normal(512).astype(np.float32)}, st_path)
+    st_buf = open(st_path, "rb").read()
+    hdr, _, start = ow.parse(st_buf)
+    raw = lambda n: ow.to_f32(ow.tensor_bytes(st_buf, hdr, start, n), hdr[n]["dtype"])
+    x = rng.standard_normal((256, 576)).astype(np.float32)
+    cases.append({"name": "st_linear", "form": "st_linear", "file": st_path, "base": "blocks.0.self_attn.qkv.",
+                  "M": 256, "x": _save(d, "stx.bin", x)})
+    refs["st_linear"] = ol.linear_torch_fp32(x, raw("blocks.0.self_attn.qkv.weight").reshape(1728, 576),
+                                             np.zeros(256 * 1728, np.float32), M=256, N=1728, K=576,
+                                             bias=raw("blocks.0.self_attn.qkv.bias")).reshape(256, 1728)
+    ids = [0, 2999, 17, 17, 1234]
+    cases.append({"name": "st_rows", "form": "st_rows", "file": st_path, "table": "shared.weight", "ids": ids,
+                  "exact": True})
+    refs["st_rows"] = ow.rows(ow.tensor_bytes(st_buf, hdr, start, "shared.weight"), "F32", 3000, 768, ids)
+    cases.append({"name": "st_conv3", "form": "st_conv3", "file": st_path, "base": "decoder.conv_in.", "cinPad": 8,
+                  "exact": True})
+    refs["st_conv3"] = ow.conv3_pack(raw("decoder.conv_in.weight"), 512, 4, 8)
+    cases.append({"name": "st_f32", "form": "st_f32", "file": st_path, "tensor": "blocks.0.mlp.0.weight",
+                  "exact": True})
+    refs["st_f32"] = raw("blocks.0.mlp.0.weight")
+    bf = np.arange(65536, dtype="<u2").tobytes()
+    cases.append({"name": "st_to_f32", "form": "st_to_f32", "raw": _save(d, "bf16.bin", np.frombuffer(bf, np.uint8)),
+                  "dtype": "BF16", "exact": True})
+    refs["st_to_f32"] = ow.to_f32(bf, "BF16")
+
     with open(os.path.join(d, "manifest.json"), "w") as f:
         json.dump({"cases": cases}, f)
     print("[node gpu] running", [c["name"] for c in cases], flush=True)
@@ -113,5 +149,9 @@ def test_reference_call_forms_through_node(tmp_path):
     for case in cases:
         got = np.fromfile(os.path.join(d, case["name"] + ".out.bin"), dtype=np.float32)
         ref = refs[case["name"]]
+        if case.get("exact"):  # decoded weights: bit for bit
+            np.testing.assert_array_equal(got.view(np.uint32), np.ascontiguousarray(ref, np.float32).reshape(-1).view(np.uint32),
+                                          err_msg=case["name"])
+            continue
         e = orc.errors(got.reshape(ref.shape), ref)
         assert e["finite"] and e["rel_l2"] <= 1e-5 and e["max_rel"] <= 1e-5, f"{case['name']}: {e}"
