@@ -11,6 +11,8 @@ The same JSON line carries:
   per_config   us/call and TFLOP/s of the other single-call configs (DiT cross, T5, VAE)
   roofline     the dominant kernel (sweep self-attention), timed per launch with HIP events
   cpu_baseline the PyTorch fp32 CPU formulation of tools/reference.py:72-79 on a bounded sample
+  callsite / linear / vae_block / weights  the callers and data either side of the operator: batched
+               DiT call sites, the DiT linears, the VAE mid-block in one call, the safetensors loader
 
     python bench.py [--steps 50] [--warmup 20] [--cpu-seconds 12] [--no-cpu]
 
@@ -214,7 +216,188 @@ def vae_block_timing(dev, calls: int = 200) -> dict:
             "flops_per_call": call.flops()}
 
 
+def dit_checkpoint() -> dict:
+    """The DiT weight file's float32 tensors (app/models/dit.js:67-104, names as
+    tools/build_models.py writes them), seeded N(0, 1/K): 14 blocks of adaLN + seven linears, plus
+    the embeddings and the final layer."""
+    import numpy as np
+
+    D, F, depth = 576, 2304, 14
+    rng = np.random.default_rng(50)
+    pool = rng.standard_normal(1 << 22, dtype=np.float32)  # windows of one seeded pool (fast to build)
+    t = {}
+
+    def draw(shape, scale):
+        n = int(np.prod(shape))  # every tensor here is smaller than the pool
+        start = int(rng.integers(0, pool.size - n + 1))
+        return (pool[start:start + n] * np.float32(scale)).reshape(shape)
+
+    def lin(name, n, k):
+        t[name + "weight"] = draw((n, k), 1 / np.sqrt(k))
+        t[name + "bias"] = draw((n,), 0.1)
+
+    lin("x_embed.", D, 16)
+    lin("t_embed.mlp.0.", D, 256)
+    lin("t_embed.mlp.2.", D, D)
+    lin("ctx_proj.", D, 768)
+    t["pos_embed"] = draw((1, 256, D), 1.0)
+    for i in range(depth):
+        p = f"blocks.{i}."
+        for name, n, k in (("adaln.1.", 6 * D, D), ("self_attn.qkv.", 3 * D, D), ("self_attn.proj.", D, D),
+                           ("cross_attn.q.", D, D), ("cross_attn.kv.", 2 * D, D), ("cross_attn.proj.", D, D),
+                           ("mlp.0.", F, D), ("mlp.2.", D, F)):
+            lin(p + name, n, k)
+    lin("final.adaln.1.", 2 * D, D)
+    lin("final.linear.", 16, D)
+    return t
+
+
+def weights_load(dev, reps: int = 10, cpu: bool = True) -> dict:
+    """The safetensors loader (app/weights.js) on a DiT-shaped checkpoint: bulk upload of the data
+    section (PCIe-inclusive), the device decode kernels against the HBM roofline, and a whole load
+    (open, upload, every tensor decoded into its own buffer) as the model loader issues it."""
+    import shutil
+    import tempfile
+
+    import numpy as np
+    import torch
+    from safetensors.numpy import save_file
+
+    from supra_attn import _lib
+    from supra_attn.weights import PinnedBuffer, SafeTensors
+
+    lib = _lib.load()
+    tensors = dit_checkpoint()
+    # the same checkpoint in bfloat16 (round to nearest even through torch), for the decode kernel
+    bf16 = {k: torch.from_numpy(v).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16) for k, v in tensors.items()}
+    tmp = tempfile.mkdtemp(prefix="sa_weights_")
+    try:
+        f32_path, bf_path = os.path.join(tmp, "dit_f32.safetensors"), os.path.join(tmp, "dit_bf16.safetensors")
+        save_file(tensors, f32_path, metadata={"format": "pt"})
+        # a BF16 file with the same header layout: written by hand (NumPy has no bfloat16)
+        header, off, blobs = {}, 0, []
+        for k, v in bf16.items():
+            header[k] = {"dtype": "BF16", "shape": list(v.shape), "data_offsets": [off, off + v.nbytes]}
+            off += v.nbytes
+            blobs.append(v.tobytes())
+        hj = json.dumps(header).encode()
+        hj += b" " * (-len(hj) % 8)
+        with open(bf_path, "wb") as f:
+            f.write(len(hj).to_bytes(8, "little") + hj)
+            for b in blobs:
+                f.write(b)
+        n_tensors = len(tensors)
+        numel = sum(v.size for v in tensors.values())
+        log(f"weights: DiT checkpoint {n_tensors} tensors, {numel} parameters")
+
+        out = {"workload": f"DiT checkpoint ({n_tensors} tensors, {numel} float32 parameters, "
+                           f"{4 * numel / 1e6:.1f} MB; the reference ships float32)"}
+        st = SafeTensors.open(f32_path)
+        nbytes = st.data_bytes
+        dst = dev.empty([nbytes], np.uint8)
+        pinned = PinnedBuffer(64 << 20)
+        for mode in ("staged", "pageable"):
+            ts = []
+            for _ in range(3):
+                t0 = time.perf_counter()
+                _lib.check(lib.sa_st_upload(st._h, 0, nbytes, dst.ptr, pinned.ptr if mode == "staged" else None,
+                                            pinned.nbytes if mode == "staged" else 0, dev.stream))
+                ts.append(time.perf_counter() - t0)
+            out[f"upload_{mode}_gbs"] = round(nbytes / min(ts) / 1e9, 2)
+        pinned.release()
+        dst.release()
+        st.close()
+
+        # decode kernels: the whole data section as one array (BF16 -> f32, F32 -> f32) and the
+        # per-tensor launches a model load issues
+        with SafeTensors.open(bf_path) as sb:
+            res = sb.resident(dev)
+            n = sb.data_bytes // 2
+            outbuf = dev.empty([n], np.float32)
+            launch = lambda: _lib.check(lib.sa_to_f32(res.ptr, _lib.SA_DT["BF16"], n, outbuf.ptr, dev.stream))
+            ms = time_calls(dev, launch, reps, warmup=3)
+            moved = n * 2 + n * 4
+            out["decode_bf16"] = {"elements": n, "us_per_launch": round(ms * 1e3, 2),
+                                  "gbs": round(moved / (ms * 1e-3) / 1e9, 1),
+                                  "frac_hbm": round(moved / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                                  "bytes_per_launch": moved}
+            outbuf2 = dev.empty([n], np.float32)
+            launch32 = lambda: _lib.check(lib.sa_to_f32(outbuf.ptr, _lib.SA_DT["F32"], n, outbuf2.ptr, dev.stream))
+            ms32 = time_calls(dev, launch32, reps, warmup=3)
+            out["decode_f32"] = {"elements": n, "us_per_launch": round(ms32 * 1e3, 2),
+                                 "gbs": round(8 * n / (ms32 * 1e-3) / 1e9, 1),
+                                 "frac_hbm": round(8 * n / (ms32 * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+            outbuf2.release()
+            names = sb.names()
+            infos = [sb.raw_info(k) for k in names]
+            offs = np.cumsum([0] + [int(t.numel) for t in infos])
+
+            def per_tensor():
+                for t, o in zip(infos, offs):
+                    _lib.check(lib.sa_to_f32(res.ptr + int(t.begin), t.dtype, t.numel, outbuf.ptr + 4 * int(o),
+                                             dev.stream))
+
+            ms_pt = time_calls(dev, per_tensor, reps, warmup=2)
+            out["decode_bf16_per_tensor"] = {"launches": len(infos), "us_total": round(ms_pt * 1e3, 1),
+                                             "gbs": round(moved / (ms_pt * 1e-3) / 1e9, 1)}
+            outbuf.release()
+
+        # a whole load as app/models/dit.js issues it: open, bulk upload, one decode per tensor
+        # into its own buffer (uploadLinear / uploadVector), synchronized
+        dev.sync()
+        t0 = time.perf_counter()
+        with SafeTensors.open(f32_path) as s2:
+            bufs = [s2.f32(dev, k) for k in s2.names()]
+            dev.sync()
+            load_s = time.perf_counter() - t0
+        for b in bufs:
+            b.release()
+        out["load_ms"] = round(load_s * 1e3, 1)
+        out["load_gbs"] = round(4 * numel / load_s / 1e9, 2)
+        if cpu:
+            # the reference decodes on the CPU (toF32); the oracle's NumPy restatement over the
+            # BF16 checkpoint's tensors, all of them (about 0.2 GB of input)
+            from oracle import weights as ow
+
+            raw = [v.tobytes() for v in bf16.values()]
+            t0 = time.perf_counter()
+            for r in raw:
+                ow.to_f32(r, "BF16")
+            dt = time.perf_counter() - t0
+            out["cpu_baseline"] = {"decode_bf16_ms": round(dt * 1e3, 1),
+                                   "gbs": round(6 * numel / dt / 1e9, 2), "cores": 1, "kind": "port",
+                                   "sample": "every tensor of the BF16 checkpoint through oracle.weights.to_f32"}
+        return out
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+
+
 COPY_BYTES = 256 << 20
+
+
+def profile_decode(dev, launches: int) -> int:
+    """`launches` BF16 -> float32 decodes of the DiT checkpoint's size (102.5 M elements), then the
+    calibration copies."""
+    import ctypes
+
+    import numpy as np
+
+    from supra_attn import _lib
+
+    n = sum(v.size for v in dit_checkpoint().values())
+    src, dst = dev.empty([n], np.uint16), dev.empty([n], np.float32)
+    src.fill_bytes(0x3F)
+    log(f"profile weights_bf16: {launches} decodes of {n} elements, {6 * n} algorithmic bytes per launch")
+    for _ in range(launches):
+        _lib.check(_lib.load().sa_to_f32(src.ptr, _lib.SA_DT["BF16"], n, dst.ptr, dev.stream))
+    dev.sync()
+    a, b = dev.empty((COPY_BYTES // 4,)), dev.empty((COPY_BYTES // 4,))
+    a.fill_bytes(0)
+    for _ in range(4):
+        _lib.check(_lib.load().sa_memcpy_d2d(b.ptr, a.ptr, COPY_BYTES, ctypes.c_void_p(dev.stream)))
+    dev.sync()
+    log(f"profile weights_bf16: done ({COPY_BYTES} bytes per calibration copy)")
+    return 0
 
 
 def profile_run(workload: str, launches: int) -> int:
@@ -225,6 +408,8 @@ def profile_run(workload: str, launches: int) -> int:
     from supra_attn.runner import Staged
 
     dev = Device(0)
+    if workload == "weights_bf16":
+        return profile_decode(dev, launches)
     if workload == "vae_block":
         from supra_attn.linear_workloads import vae_block
         from supra_attn.runner import StagedVae
@@ -348,6 +533,12 @@ def main() -> int:
     log(f"linears, one block at batch 64: {linear['block_us']:.1f} us, {linear['block_tflops']:.1f} TFLOP/s "
         + " ".join(f"{k} {v['us']:.0f}us" for k, v in linear["layers"].items()))
 
+    # the weight loader feeding those linears (app/weights.js): upload, device decode, whole load
+    weights = weights_load(dev, cpu=not args.no_cpu)
+    log(f"weights: upload {weights['upload_staged_gbs']} GB/s staged, {weights['upload_pageable_gbs']} GB/s pageable; "
+        f"bf16 decode {weights['decode_bf16']['us_per_launch']} us ({weights['decode_bf16']['gbs']} GB/s); "
+        f"whole load {weights['load_ms']} ms")
+
     # single-call configs
     per_config = {}
     for name, make in workloads.CONFIGS.items():
@@ -428,6 +619,7 @@ def main() -> int:
         "callsite": callsite,
         "linear": linear,
         "vae_block": vae,
+        "weights": weights,
         "cpu_baseline": None if cpu is None else {k: (round(v, 6) if isinstance(v, float) else v) for k, v in cpu.items()},
     }
     print(json.dumps(result))

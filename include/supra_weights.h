@@ -82,8 +82,9 @@ const void* sa_st_data(const sa_st_file* file);    /* host address of the data s
 
 /* Copies bytes [begin, end) of the data section to device memory at dst, and returns when the copy
  * has completed. With `staging` (pinned host memory from hipHostMalloc, at least 2 MiB) the copy
- * runs in chunks through the two halves of it, so that filling one half from the file overlaps the
- * DMA of the other; with staging == NULL the runtime copies from the mapping itself. */
+ * runs in chunks through the two halves of it, so that filling one half from the file (several host
+ * threads) overlaps the DMA of the other; with staging == NULL the runtime copies from the mapping
+ * itself. */
 int sa_st_upload(const sa_st_file* file, int64_t begin, int64_t end, void* dst, void* staging,
                  int64_t staging_bytes, void* stream);
 

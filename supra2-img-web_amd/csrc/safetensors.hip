@@ -20,6 +20,7 @@
 
 #include <algorithm>
 #include <string>
+#include <thread>
 #include <unordered_map>
 #include <utility>
 #include <vector>
@@ -325,6 +326,25 @@ int parse(sa_st_file* f) {
   return ok();
 }
 
+// memcpy split over up to kCopyThreads host threads (slices of at least 1 MiB): one thread cannot
+// read a page-cache mapping as fast as the DMA drains pinned memory.
+constexpr int kCopyThreads = 8;
+
+void parallel_copy(uint8_t* dst, const uint8_t* src, int64_t len) {
+  constexpr int64_t kMinSlice = 1 << 20;
+  const int64_t want = std::min<int64_t>(kCopyThreads, std::max<int64_t>(1, len / kMinSlice));
+  const int64_t slice = ((len + want - 1) / want + 4095) & ~(int64_t)4095;
+  std::vector<std::thread> pool;
+  pool.reserve((size_t)want);
+  int64_t off = slice;
+  for (; off < len; off += slice) {
+    const int64_t n = std::min(slice, len - off);
+    pool.emplace_back([=] { memcpy(dst + off, src + off, (size_t)n); });
+  }
+  memcpy(dst, src, (size_t)std::min(slice, len));
+  for (std::thread& t : pool) t.join();
+}
+
 int finish_open(sa_st_file* f, sa_st_file** out) {
   const int rc = parse(f);
   if (rc != SA_OK) {
@@ -456,7 +476,7 @@ int sa_st_upload(const sa_st_file* f, int64_t begin, int64_t end, void* dst, voi
     uint8_t* stage = static_cast<uint8_t*>(staging) + b * half;
     if (i >= 2) e = hipEventSynchronize(done[b]);
     if (e != hipSuccess) break;
-    memcpy(stage, src + off, (size_t)len);
+    parallel_copy(stage, src + off, len);
     e = hipMemcpyAsync(static_cast<uint8_t*>(dst) + off, stage, (size_t)len, hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = hipEventRecord(done[b], s);
   }

@@ -28,7 +28,6 @@ constexpr uint32_t kCanonicalNaN = 0x7fc00000u;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 int dtype_bytes(int32_t dt) {
   switch (dt) {
@@ -90,52 +89,66 @@ __device__ __forceinline__ typename Raw<DT>::T load_bytes(const uint8_t* p) {
 }
 
 constexpr int kThreads = 256;
-constexpr int kUnroll = 4;  // 16-byte packs in flight per thread
 
-// dst[i] = decode(src[i]) for i < n. Elements [0, head) and [head + packs*P, n) one per thread;
-// the middle as 16-byte packs of P = 16 / sizeof(T) elements (src + head*sizeof(T) is 16-byte
-// aligned), stored as float4 when DST16 (dst + head is 16-byte aligned), else as single floats.
-template <int DT, bool DST16>
-__global__ __launch_bounds__(kThreads) void to_f32_kernel(const uint8_t* __restrict__ src, float* __restrict__ dst,
-                                                          int64_t n, int64_t head, int64_t packs) {
+// Quads (4 consecutive elements, one float4 of output) per thread and pass: 64 source bytes in
+// flight per lane whatever the element size.
+template <int DT>
+constexpr int kQuadsPerThread = 16 / (int)sizeof(typename Raw<DT>::T);
+
+// Four consecutive elements from p (element-aligned); VEC: p is aligned to min(4 * sizeof(T), 16)
+// bytes, so the four come in one (two, for 8-byte types) vector loads.
+template <int DT, bool VEC>
+__device__ __forceinline__ void load_quad(const typename Raw<DT>::T* p, typename Raw<DT>::T (&e)[4]) {
   using T = typename Raw<DT>::T;
-  constexpr int P = 16 / (int)sizeof(T);
+  if constexpr (VEC && sizeof(T) == 1) {
+    const uint32_t v = *reinterpret_cast<const uint32_t*>(p);
+    __builtin_memcpy(e, &v, 4);
+  } else if constexpr (VEC && sizeof(T) == 2) {
+    const uint2 v = *reinterpret_cast<const uint2*>(p);
+    __builtin_memcpy(e, &v, 8);
+  } else if constexpr (VEC && sizeof(T) == 4) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+    __builtin_memcpy(e, &v, 16);
+  } else if constexpr (VEC && sizeof(T) == 8) {
+    const u32x4 a = reinterpret_cast<const u32x4*>(p)[0];
+    const u32x4 b = reinterpret_cast<const u32x4*>(p)[1];
+    __builtin_memcpy(e, &a, 16);
+    __builtin_memcpy(e + 2, &b, 16);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) e[i] = p[i];
+  }
+}
+
+// dst[i] = decode(src[i]) for i < n. Elements [0, head) and [head + 4*quads, n) one per thread;
+// the middle as quads: lane j of a pass writes output float4 j, so every store instruction of a
+// wave covers 1 KiB of whole lines (dst + head is 16-byte aligned), and every load instruction
+// reads the matching contiguous source bytes.
+template <int DT, bool VEC>
+__global__ __launch_bounds__(kThreads) void to_f32_kernel(const uint8_t* __restrict__ src, float* __restrict__ dst,
+                                                          int64_t n, int64_t head, int64_t quads) {
+  using T = typename Raw<DT>::T;
+  constexpr int U = kQuadsPerThread<DT>;
   const int64_t tid = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   const int64_t nthreads = (int64_t)gridDim.x * kThreads;
   const T* s = reinterpret_cast<const T*>(src);
-  const int64_t tail0 = head + packs * P;
+  const int64_t tail0 = head + quads * 4;
   for (int64_t i = tid; i < head; i += nthreads) dst[i] = decode<DT>(s[i]);
   for (int64_t i = tail0 + tid; i < n; i += nthreads) dst[i] = decode<DT>(s[i]);
 
-  const u32x4* sv = reinterpret_cast<const u32x4*>(src + head * (int64_t)sizeof(T));
-  float* d = dst + head;
-  for (int64_t base = tid; base < packs; base += nthreads * kUnroll) {
-    u32x4 v[kUnroll];
+  const T* sq = s + head;
+  f32x4* dq = reinterpret_cast<f32x4*>(dst + head);
+  for (int64_t base = tid; base < quads; base += nthreads * U) {
+    T e[U][4];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int64_t k = base + (int64_t)u * nthreads;
-      if (k < packs) v[u] = __builtin_nontemporal_load(sv + k);
+      if (k < quads) load_quad<DT, VEC>(sq + 4 * k, e[u]);
     }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int64_t k = base + (int64_t)u * nthreads;
-      if (k >= packs) break;
-      T e[P];
-      __builtin_memcpy(e, &v[u], 16);
-      float* o = d + k * P;
-      if constexpr (DST16 && P == 2) {
-        const f32x2 f = {decode<DT>(e[0]), decode<DT>(e[1])};
-        __builtin_nontemporal_store(f, reinterpret_cast<f32x2*>(o));
-      } else if constexpr (DST16) {
-#pragma unroll
-        for (int q = 0; q < P; q += 4) {
-          const f32x4 f = {decode<DT>(e[q]), decode<DT>(e[q + 1]), decode<DT>(e[q + 2]), decode<DT>(e[q + 3])};
-          __builtin_nontemporal_store(f, reinterpret_cast<f32x4*>(o + q));
-        }
-      } else {
-#pragma unroll
-        for (int q = 0; q < P; ++q) o[q] = decode<DT>(e[q]);
-      }
+      if (k < quads) dq[k] = f32x4{decode<DT>(e[u][0]), decode<DT>(e[u][1]), decode<DT>(e[u][2]), decode<DT>(e[u][3])};
     }
   }
 }
@@ -200,19 +213,23 @@ int grid_for(int64_t work_items) {
 template <int DT>
 hipError_t launch_to_f32(const uint8_t* src, float* dst, int64_t n, hipStream_t stream) {
   using T = typename Raw<DT>::T;
-  constexpr int64_t P = 16 / sizeof(T);
   if ((uintptr_t)src % sizeof(T) != 0) {
     hipLaunchKernelGGL(to_f32_bytes_kernel<DT>, dim3(grid_for(n)), dim3(kThreads), 0, stream, src, dst, n);
     return hipGetLastError();
   }
-  int64_t head = (int64_t)((16 - (uintptr_t)src % 16) % 16) / (int64_t)sizeof(T);
+  int64_t head = (int64_t)((16 - (uintptr_t)dst % 16) % 16) / 4;  // dst + head is 16-byte aligned
   if (head > n) head = n;
-  const int64_t packs = (n - head) / P;
-  const bool dst16 = ((uintptr_t)(dst + head) % 16) == 0;
-  const int64_t singles = n - packs * P;  // head and tail elements
-  const dim3 grid(grid_for((packs + kUnroll - 1) / kUnroll > singles ? (packs + kUnroll - 1) / kUnroll : singles));
-  if (dst16) hipLaunchKernelGGL((to_f32_kernel<DT, true>), grid, dim3(kThreads), 0, stream, src, dst, n, head, packs);
-  else hipLaunchKernelGGL((to_f32_kernel<DT, false>), grid, dim3(kThreads), 0, stream, src, dst, n, head, packs);
+  const int64_t quads = (n - head) / 4;
+  const uintptr_t vec_align = sizeof(T) * 4 < 16 ? sizeof(T) * 4 : 16;
+  const bool vec = ((uintptr_t)(src + head * (int64_t)sizeof(T)) % vec_align) == 0;
+  constexpr int64_t U = kQuadsPerThread<DT>;
+  const int64_t singles = n - quads * 4;  // head and tail elements
+  const int64_t threads = (quads + U - 1) / U > singles ? (quads + U - 1) / U : singles;
+  int64_t blocks = (threads + kThreads - 1) / kThreads;
+  if (blocks < 1) blocks = 1;
+  if (blocks > (1 << 30)) blocks = 1 << 30;  // the loops stride over the rest
+  if (vec) hipLaunchKernelGGL((to_f32_kernel<DT, true>), dim3((unsigned)blocks), dim3(kThreads), 0, stream, src, dst, n, head, quads);
+  else hipLaunchKernelGGL((to_f32_kernel<DT, false>), dim3((unsigned)blocks), dim3(kThreads), 0, stream, src, dst, n, head, quads);
   return hipGetLastError();
 }
 
