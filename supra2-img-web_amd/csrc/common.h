@@ -9,6 +9,7 @@ namespace sa {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 // Running-max seed: finite, so that (m_old - m_new) is never (-inf) - (-inf) on rows whose keys

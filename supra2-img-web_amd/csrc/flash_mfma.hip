@@ -69,6 +69,17 @@ __device__ __forceinline__ void load_to_lds16(const float* src, float* lds_wave_
   __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)lds_wave_base, 16, 0, 0);
 }
 
+// Buffer resource over [base, base + 2 GiB): a scalar descriptor, so a copy's per-lane address is
+// a 32-bit offset and the per-step base moves on the scalar unit (no 64-bit VALU address math).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+}
+
+// As load_to_lds16, from byte offset `voff` of the buffer `r`.
+__device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t r, unsigned voff, float* lds_wave_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds_wave_base, 16, voff, 0, 0, 0);
+}
+
 constexpr float kRescaleSlack = 8.f;  // log2 units: p stays <= 256 between rescales
 
 __device__ __forceinline__ f32x16 zero16() {
@@ -158,13 +169,13 @@ __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void
     float* vt = kt + TILE;
     const int key0 = step * KT;
     if (key0 + KT <= kv_len) {
-      const char* kb = reinterpret_cast<const char*>(kbase + (int64_t)key0 * p.ldk);
-      const char* vb = reinterpret_cast<const char*>(vbase + (int64_t)key0 * p.ldv);
+      const __amdgpu_buffer_rsrc_t kr = buffer_rsrc(kbase + (int64_t)key0 * p.ldk);
+      const __amdgpu_buffer_rsrc_t vr = buffer_rsrc(vbase + (int64_t)key0 * p.ldv);
 #pragma unroll
       for (int n = 0; n < NI; ++n) {
         const int blk64 = n * 4 + wave;  // 64-chunk (1 KiB) block of the tile
-        load_to_lds16(reinterpret_cast<const float*>(kb + koff[n]), kt + blk64 * 256);
-        load_to_lds16(reinterpret_cast<const float*>(vb + voff[n]), vt + blk64 * 256);
+        buffer_to_lds16(kr, koff[n], kt + blk64 * 256);
+        buffer_to_lds16(vr, voff[n], vt + blk64 * 256);
       }
     } else {
 #pragma unroll
@@ -325,10 +336,11 @@ __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void
 #pragma unroll
         for (int t = 0; t < NDB; ++t) oacc[t] *= alpha;
       }
-      float ps = 0.f;
       float pr[16];
+      pr[0] = fast_exp2(u[0] - m);
+      float ps = pr[0];  // (not 0 + pr[0]: the compiler keeps an add of zero, for -0)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
+      for (int r = 1; r < 16; ++r) {
         pr[r] = fast_exp2(u[r] - m);
         ps += pr[r];
       }
@@ -387,7 +399,7 @@ __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void
 
   // ---- normalise and store: lane holds O[qi][32t + 8g + 4*half + 0..3] in registers 4g..4g+3
   const float lt = sum_with_partner(l);
-  const float inv = lt > 0.f ? 1.f / lt : 0.f;
+  const float inv = lt > 0.f ? __builtin_amdgcn_rcpf(lt) : 0.f;  // v_rcp_f32 (1 ulp)
   if constexpr (NSPLIT == 1) {
     // through LDS: each wave writes its 32 x D tile (16-byte chunks swizzled by row, conflict-free
     // both ways) and reads it back as whole rows, CPR lanes per row
@@ -408,13 +420,27 @@ __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void
     }
     constexpr int RPI = 64 / CPR;  // rows per store instruction
     const int rsub = lane / CPR, cidx = lane % CPR;
-    float* obase = p.o + p.o_off + (int64_t)b * p.so + h * D + 4 * cidx;
+    float* obase = p.o + p.o_off + (int64_t)b * p.so + h * D;
+    if ((int64_t)p.Lq * p.ldo < (int64_t)1 << 29) {
+      // byte offsets of every row fit in 31 bits: buffer stores from a scalar base
+      const __amdgpu_buffer_rsrc_t orsrc = buffer_rsrc(obase);
 #pragma unroll
-    for (int j = 0; j < 32 / RPI; ++j) {
-      const int row = RPI * j + rsub;
-      const f32x4 x = *reinterpret_cast<const f32x4*>(ot + row * D + 4 * (cidx ^ (row & 15)));
-      const int qrow = q0 + qg * 32 + row;
-      if (qrow < p.Lq) *reinterpret_cast<f32x4*>(obase + (int64_t)qrow * p.ldo) = x;
+      for (int j = 0; j < 32 / RPI; ++j) {
+        const int row = RPI * j + rsub;
+        const f32x4 x = *reinterpret_cast<const f32x4*>(ot + row * D + 4 * (cidx ^ (row & 15)));
+        const int qrow = q0 + qg * 32 + row;
+        if (qrow < p.Lq)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), orsrc,
+                                                     (unsigned)(qrow * (int)p.ldo + 4 * cidx) * 4u, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 32 / RPI; ++j) {
+        const int row = RPI * j + rsub;
+        const f32x4 x = *reinterpret_cast<const f32x4*>(ot + row * D + 4 * (cidx ^ (row & 15)));
+        const int qrow = q0 + qg * 32 + row;
+        if (qrow < p.Lq) *reinterpret_cast<f32x4*>(obase + (int64_t)qrow * p.ldo + 4 * cidx) = x;
+      }
     }
   } else if (q_valid) {
     float* dst = p.o + p.o_off + (int64_t)b * p.so + (int64_t)qi * p.ldo + h * D + 4 * half;
