@@ -272,7 +272,10 @@ int choose(const sa::AttnParams& p, Choice* c) {
                    p.k_off % 4 == 0 && p.v_off % 4 == 0 && p.o_off % 4 == 0 && p.ldq % 4 == 0 && p.ldk % 4 == 0 &&
                    p.ldv % 4 == 0 && p.ldo % 4 == 0 && p.sq % 4 == 0 && p.sk % 4 == 0 && p.sv % 4 == 0 &&
                    p.so % 4 == 0;
-  if ((p.D == 64 || p.D == 128) && vec) {
+  // The MFMA kernels address a copy's rows (up to 128) as 32-bit byte offsets from the block's
+  // first row; longer strides take the generic kernel, whose addresses are 64-bit.
+  const bool off32 = p.ldk < ((int64_t)1 << 22) && p.ldv < ((int64_t)1 << 22);
+  if ((p.D == 64 || p.D == 128) && vec && off32) {
     // Units of 32 queries; below ~2 waves per SIMD (256 CUs x 4 SIMDs) split the key blocks
     // across the waves of a workgroup so that more SIMDs get work.
     const int64_t units = (int64_t)p.B * p.H * ((p.Lq + 31) / 32);
@@ -285,7 +288,7 @@ int choose(const sa::AttnParams& p, Choice* c) {
     c->name = sa::flash_mfma_name(p.D, nsplit);
     return SA_OK;
   }
-  if (vec && sa::wide_mfma_supported(p)) {
+  if (vec && off32 && sa::wide_mfma_supported(p)) {
     c->path = Path::kWide;
     c->nsplit = 1;
     c->wide = sa::wide_mfma_plan(p, num_cus());

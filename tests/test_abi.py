@@ -94,6 +94,14 @@ def test_valid_call_selects_mfma_kernel():
     assert _lib.kernel_name(good_args(D=128, H=4, ldo=512, so=256 * 512)) == "flash_mfma_d128_split2"
 
 
+def test_generic_kernel_for_row_strides_beyond_32bit_copy_offsets():
+    big = 1 << 22  # 128 rows of this stride no longer fit a 31-bit byte offset
+    far = FAKE + (1 << 40)  # an output beyond the long k/v extents
+    assert _lib.kernel_name(good_args(ldk=big - 4, ldv=big - 4, sk=256 * big, sv=256 * big, o=far)) == "flash_mfma_d64_split4"
+    assert _lib.kernel_name(good_args(ldk=big, ldv=1728, sk=256 * big, o=far)) == "generic"
+    assert _lib.kernel_name(good_args(ldv=big, sv=256 * big, o=far)) == "generic"
+
+
 def test_generic_kernel_for_other_head_dims_and_unaligned_rows():
     assert _lib.kernel_name(good_args(D=32, ldo=288, so=256 * 288)) == "generic"
     assert _lib.kernel_name(good_args(q_off=1)) == "generic"
