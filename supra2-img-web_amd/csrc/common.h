@@ -39,4 +39,24 @@ __device__ __forceinline__ float sum_with_partner(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) const void global_void_t;
+
+// Moves 16 bytes per lane from global memory to LDS: lane i writes lds_wave_base + 16*i.
+__device__ __forceinline__ void load_to_lds16(const void* src, float* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)lds_wave_base, 16, 0, 0);
+}
+
+// Buffer resource over [base, base + 2 GiB): a scalar descriptor, so a copy's per-lane address is
+// a 32-bit offset and a per-block base moves on the scalar unit (no 64-bit VALU address math).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+}
+
+// As load_to_lds16, from byte offset `voff` (per lane) + `soff` (uniform) of the buffer `r`.
+__device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t r, unsigned voff, float* lds_wave_base,
+                                                unsigned soff = 0) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds_wave_base, 16, voff, soff, 0, 0);
+}
+
 }  // namespace sa

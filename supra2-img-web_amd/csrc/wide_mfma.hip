@@ -27,12 +27,6 @@ namespace sa {
 
 namespace {
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) const void global_void_t;
-
-__device__ __forceinline__ void load_to_lds16(const float* src, float* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)lds_wave_base, 16, 0, 0);
-}
 
 constexpr float kRescaleSlack = 8.f;
 
