@@ -214,15 +214,22 @@ __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void
   // ---- Q into registers, pre-scaled: lane holds scale*log2(e)*Q[qi][8i + 4*half + j] in qr[4i + j]
   float qr[QREG];
   {
-    const float* src = p.q + p.q_off + (int64_t)b * p.sq + (int64_t)qi * p.ldq + h * D;
+    // unconditional loads from a clamped row (no branch per load); rows past Lq are zeroed after
+    const float* src = p.q + p.q_off + (int64_t)b * p.sq + (int64_t)min(qi, p.Lq - 1) * p.ldq + h * D;
+    f32x4 xq[QREG / 4];
+#pragma unroll
+    for (int i = 0; i < QREG / 4; ++i) xq[i] = *reinterpret_cast<const f32x4*>(src + 4 * (2 * i + half));
+    // Stage 1 is unused until the loop: the second step's tile streams in from the start too,
+    // rather than after the first barrier (which left the two-step loops of the key-split
+    // kernels waiting for their second tile).
+    if (nstep > 1) issue(1, 1);
 #pragma unroll
     for (int i = 0; i < QREG / 4; ++i) {
-      f32x4 x = {0.f, 0.f, 0.f, 0.f};
-      if (q_valid) x = *reinterpret_cast<const f32x4*>(src + 4 * (2 * i + half));
-      qr[4 * i + 0] = x[0] * p.scale_log2;
-      qr[4 * i + 1] = x[1] * p.scale_log2;
-      qr[4 * i + 2] = x[2] * p.scale_log2;
-      qr[4 * i + 3] = x[3] * p.scale_log2;
+      const float sc = q_valid ? p.scale_log2 : 0.f;
+      qr[4 * i + 0] = xq[i][0] * sc;
+      qr[4 * i + 1] = xq[i][1] * sc;
+      qr[4 * i + 2] = xq[i][2] * sc;
+      qr[4 * i + 3] = xq[i][3] * sc;
     }
   }
 
@@ -230,10 +237,11 @@ __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void
   for (int step = 0; step < nstep; ++step) {
     const int buf = step & 1;
     // stage `buf` has landed for this thread; the barrier makes it whole, and every wave has
-    // finished reading stage buf^1 (the previous step), which the next issue overwrites
+    // finished reading stage buf^1 (the previous step), which the next issue (from step 1 on:
+    // step 1 itself was issued before the loop) overwrites
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (step + 1 < nstep) issue(step + 1, buf ^ 1);
+    if (step >= 1 && step + 1 < nstep) issue(step + 1, buf ^ 1);
     const int blk = step * NSPLIT + ks;
     if (blk < nblk) {
       const int k0 = blk * 32;

@@ -27,15 +27,8 @@ namespace sa {
 
 namespace {
 
-
 constexpr float kRescaleSlack = 8.f;
 
-// s_waitcnt with vmcnt <= N (expcnt and lgkmcnt left unconstrained), gfx9 encoding.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
 
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;
