@@ -8,7 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <math.h>
-#include <mutex>
+#include <atomic>
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -236,13 +236,9 @@ struct Choice {
   const char* name;
 };
 
-// ---- per-device state: CU count
+// ---- per-device state: CU count (0 until queried; concurrent first calls query it twice, harmlessly)
 constexpr int kMaxDevices = 64;
-struct DeviceState {
-  int num_cus = 0;
-};
-std::mutex g_dev_mutex;
-DeviceState g_dev[kMaxDevices];
+std::atomic<int> g_num_cus[kMaxDevices];
 
 int current_device() {
   int dev = 0;
@@ -255,14 +251,11 @@ int current_device() {
 int num_cus() {
   const int dev = current_device();
   if (dev < 0) return 256;
-  std::lock_guard<std::mutex> lock(g_dev_mutex);
-  DeviceState& st = g_dev[dev];
-  if (st.num_cus == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
-    st.num_cus = n;
-  }
-  return st.num_cus;
+  int n = g_num_cus[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
+  g_num_cus[dev].store(n, std::memory_order_relaxed);
+  return n;
 }
 
 // Kernel selection. The MFMA kernels need D in {64, 128} and 16-byte aligned rows (the same gate

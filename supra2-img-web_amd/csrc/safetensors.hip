@@ -19,6 +19,8 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <exception>
+#include <new>
 #include <string>
 #include <thread>
 #include <unordered_map>
@@ -335,18 +337,30 @@ void parallel_copy(uint8_t* dst, const uint8_t* src, int64_t len) {
   const int64_t want = std::min<int64_t>(kCopyThreads, std::max<int64_t>(1, len / kMinSlice));
   const int64_t slice = ((len + want - 1) / want + 4095) & ~(int64_t)4095;
   std::vector<std::thread> pool;
-  pool.reserve((size_t)want);
-  int64_t off = slice;
-  for (; off < len; off += slice) {
-    const int64_t n = std::min(slice, len - off);
-    pool.emplace_back([=] { memcpy(dst + off, src + off, (size_t)n); });
+  int64_t done = slice;  // bytes [slice, done) are handed to started threads
+  try {
+    pool.reserve((size_t)want);
+    for (; done < len; done += slice) {
+      const int64_t off = done, n = std::min(slice, len - done);
+      pool.emplace_back([=] { memcpy(dst + off, src + off, (size_t)n); });
+    }
+  } catch (...) {
+    // a thread could not start: this thread copies what was not handed out
   }
   memcpy(dst, src, (size_t)std::min(slice, len));
+  if (done < len) memcpy(dst + done, src + done, (size_t)(len - done));
   for (std::thread& t : pool) t.join();
 }
 
 int finish_open(sa_st_file* f, sa_st_file** out) {
-  const int rc = parse(f);
+  int rc;
+  try {
+    rc = parse(f);
+  } catch (...) {
+    if (f->map) munmap(f->map, (size_t)f->size);
+    delete f;
+    throw;
+  }
   if (rc != SA_OK) {
     if (f->map) munmap(f->map, (size_t)f->size);
     delete f;
@@ -356,11 +370,41 @@ int finish_open(sa_st_file* f, sa_st_file** out) {
   return ok();
 }
 
+int open_file(const char* path, sa_st_file** out);
+int open_memory(const void* bytes, int64_t size, sa_st_file** out);
+int upload(const sa_st_file* f, int64_t begin, int64_t end, void* dst, void* staging, int64_t staging_bytes,
+           void* stream);
+
+// Runs `body` and turns a C++ exception (host allocation failure) into an error status: nothing
+// propagates across the C ABI.
+template <class F>
+int guarded(F body) {
+  try {
+    return body();
+  } catch (const std::exception& e) {
+    return fail(SA_ERR_IO, "host allocation failed: %s", e.what());
+  } catch (...) {
+    return fail(SA_ERR_IO, "host allocation failed");
+  }
+}
+
 }  // namespace
 
 extern "C" {
 
 int sa_st_open(const char* path, sa_st_file** out) {
+  return guarded([&] { return open_file(path, out); });
+}
+
+int sa_st_open_memory(const void* bytes, int64_t size, sa_st_file** out) {
+  return guarded([&] { return open_memory(bytes, size, out); });
+}
+
+}  // extern "C"
+
+namespace {
+
+int open_file(const char* path, sa_st_file** out) {
   if (!out) return fail(SA_ERR_INVALID, "out is NULL");
   *out = nullptr;
   if (!path) return fail(SA_ERR_INVALID, "path is NULL");
@@ -381,22 +425,31 @@ int sa_st_open(const char* path, sa_st_file** out) {
   close(fd);
   if (map == MAP_FAILED) return fail(SA_ERR_IO, "mmap %s: %s", path, strerror(e));
   madvise(map, (size_t)st.st_size, MADV_SEQUENTIAL);
-  sa_st_file* f = new sa_st_file;
+  sa_st_file* f = new (std::nothrow) sa_st_file;
+  if (!f) {
+    munmap(map, (size_t)st.st_size);
+    return fail(SA_ERR_IO, "out of host memory");
+  }
   f->base = static_cast<const uint8_t*>(map);
   f->size = st.st_size;
   f->map = map;
   return finish_open(f, out);
 }
 
-int sa_st_open_memory(const void* bytes, int64_t size, sa_st_file** out) {
+int open_memory(const void* bytes, int64_t size, sa_st_file** out) {
   if (!out) return fail(SA_ERR_INVALID, "out is NULL");
   *out = nullptr;
   if (!bytes || size < 0) return fail(SA_ERR_INVALID, "bytes is NULL or size is negative");
-  sa_st_file* f = new sa_st_file;
+  sa_st_file* f = new (std::nothrow) sa_st_file;
+  if (!f) return fail(SA_ERR_IO, "out of host memory");
   f->base = static_cast<const uint8_t*>(bytes);
   f->size = size;
   return finish_open(f, out);
 }
+
+}  // namespace
+
+extern "C" {
 
 int sa_st_close(sa_st_file* f) {
   if (!f) return ok();
@@ -416,10 +469,12 @@ int sa_st_info(const sa_st_file* f, const char* name, sa_st_tensor* out) {
   if (!f || !name || !out) return fail(SA_ERR_INVALID, "NULL argument");
   if (out->struct_size != sizeof(sa_st_tensor))
     return fail(SA_ERR_INVALID, "struct_size %u != sizeof(sa_st_tensor) %zu", out->struct_size, sizeof(sa_st_tensor));
-  auto it = f->index.find(name);
-  if (it == f->index.end()) return fail(SA_ERR_NOT_FOUND, "missing tensor %s", name);
-  *out = f->tensors[it->second].second;
-  return ok();
+  return guarded([&] {
+    auto it = f->index.find(name);
+    if (it == f->index.end()) return fail(SA_ERR_NOT_FOUND, "missing tensor %s", name);
+    *out = f->tensors[it->second].second;
+    return ok();
+  });
 }
 
 int64_t sa_st_metadata_count(const sa_st_file* f) { return f ? (int64_t)f->meta.size() : 0; }
@@ -442,6 +497,15 @@ const void* sa_st_data(const sa_st_file* f) { return f ? f->base + f->data_start
 
 int sa_st_upload(const sa_st_file* f, int64_t begin, int64_t end, void* dst, void* staging, int64_t staging_bytes,
                  void* stream) {
+  return guarded([&] { return upload(f, begin, end, dst, staging, staging_bytes, stream); });
+}
+
+}  // extern "C"
+
+namespace {
+
+int upload(const sa_st_file* f, int64_t begin, int64_t end, void* dst, void* staging, int64_t staging_bytes,
+           void* stream) {
   if (!f) return fail(SA_ERR_INVALID, "file is NULL");
   const int64_t data_bytes = f->size - f->data_start;
   if (begin < 0 || begin > end || end > data_bytes)
@@ -487,4 +551,4 @@ int sa_st_upload(const sa_st_file* f, int64_t begin, int64_t end, void* dst, voi
   return e == hipSuccess ? ok() : sa::hip_fail(e, "staged upload");
 }
 
-}  // extern "C"
+}  // namespace
