@@ -68,13 +68,6 @@ __device__ __forceinline__ float apply_act(float v) {
   return v;
 }
 
-// s_waitcnt with vmcnt <= N (expcnt and lgkmcnt left unconstrained), gfx9 encoding.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
 // WM x WN accumulators per wave, BK k per tile (16 or 32), NS tiles in flight (LDS stages); the
 // activation and the epilogue are compile-time, so the store loop has no per-element branches.
 template <int WM, int WN, int BK, int NS, int ACT, int EPI>
@@ -361,15 +354,24 @@ LinearTile linear_mfma_tile(const LinearParams& p, int num_cus) {
   // 350 us; 128 x 64 tiles: 286 and 368), the 576-wide layers on 64 x 64 tiles at five workgroups per
   // CU (proj/q/cproj 101 us, fc2 384 us; 128 x 64: 106 and 406). 64 x 64 tiles also spread small
   // calls (the 1024-row VAE projections, per-prompt context projections) over more CUs.
+  // Then 64 x 192 tiles (one 32 x 96 strip per wave, each x operand read feeding three MFMAs),
+  // measured per layer: qkv 283 -> 269 us (k-depth 32, 2 stages); the 576-wide layers at three
+  // workgroups per CU with k-depth 16 and 3 stages: proj/q/cproj 101 -> 99.4 us, fc2 384 -> 369 us
+  // (fc1 stays on 128 x 192: 364 us with 64 x 192).
   const int64_t tiles_wide = ((p.M + 127) / 128) * ((p.N + 191) / 192);
-  if (p.N >= 1024 && tiles_wide >= num_cus) return {2, 3};
-  return {1, 1};
+  const int64_t tiles_tall = ((p.M + 63) / 64) * ((p.N + 191) / 192);
+  if (p.N >= 2048 && tiles_wide >= num_cus) return {2, 3, 32, 2};
+  if (p.N >= 1024 && tiles_tall >= 4 * (int64_t)num_cus) return {1, 3, 32, 2};
+  if (p.N % 192 == 0 && tiles_tall >= 3 * (int64_t)num_cus) return {1, 3, 16, 3};
+  return {1, 1, 32, 2};
 }
 
 const char* linear_kernel_name(const LinearParams& p, int num_cus) {
   if (!linear_mfma_supported(p)) return "linear_generic";
   const LinearTile t = linear_mfma_tile(p, num_cus);
-  return t.wn == 3 ? "linear_mfma_128x192" : "linear_mfma_64x64";
+  if (t.wm == 2) return "linear_mfma_128x192";
+  if (t.wn == 3) return t.bk == 16 ? "linear_mfma_64x192_bk16" : "linear_mfma_64x192";
+  return "linear_mfma_64x64";
 }
 
 hipError_t launch_linear(const LinearParams& p, int num_cus, hipStream_t stream) {
@@ -380,7 +382,8 @@ hipError_t launch_linear(const LinearParams& p, int num_cus, hipStream_t stream)
     return hipGetLastError();
   }
   const LinearTile t = linear_mfma_tile(p, num_cus);
-  if (t.wn == 3) return launch_act<2, 3, 32, 2>(p, stream);
+  if (t.wm == 2) return launch_act<2, 3, 32, 2>(p, stream);
+  if (t.wn == 3) return t.bk == 16 ? launch_act<1, 3, 16, 3>(p, stream) : launch_act<1, 3, 32, 2>(p, stream);
   return launch_act<1, 1, 32, 2>(p, stream);
 }
 
