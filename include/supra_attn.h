@@ -89,7 +89,7 @@ typedef struct sa_attn_args {
   float* o;
   int64_t q_off, k_off, v_off, o_off; /* element offsets (qOff/kOff/vOff/oOff in ops.js) */
   int64_t ldq, ldk, ldv, ldo;         /* row strides; ldo <= 0 means H*D (ops.js:114) */
-  int64_t sq, sk, sv, so;             /* batch strides; ignored when B == 1 */
+  int64_t sq, sk, sv, so;             /* batch strides; ignored when B == 1. Offsets and strides < 2^40 */
   float scale;                        /* softmax scale; the JS default 1/sqrt(D) is set by callers */
   int32_t bias_mode;                  /* SA_BIAS_* */
   const float* bias;                  /* DENSE: [B?][H, Lq, Lk]; RELPOS: table [num_buckets, H] */

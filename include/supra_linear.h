@@ -37,7 +37,7 @@ extern "C" {
  * with X[m][k] = x[x_off + m*ldx + k], W[n][k] = w[n*ldw + k] (the PyTorch [out, in] weight layout
  * the reference uploads, app/weights.js:89-96), bias optional, then stored or added into
  * Y[m][n] = y[y_off + m*ldy + n] as `epilogue` says. Strides of 0 default to K (ldx, ldw) and N
- * (ldy). y must not overlap x, w, bias or gate. Set struct_size = sizeof(sa_linear_args) and
+ * (ldy); offsets and strides must be below 2^40. y must not overlap x, w, bias or gate. Set struct_size = sizeof(sa_linear_args) and
  * alpha (1 for a plain layer; the reference's default).
  */
 typedef struct sa_linear_args {

@@ -68,6 +68,11 @@ bool overlaps(const Extent& a, const Extent& b) { return a.lo < b.hi && b.lo < a
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
+// Offsets and strides (in floats) at or above 2^40 (4 TiB) are rejected, so that the extent and
+// address arithmetic below stays far from int64 overflow.
+constexpr int64_t kMaxExtent = (int64_t)1 << 40;
+bool too_large(int64_t v) { return v >= kMaxExtent; }
+
 // Resolves an sa_attn_args into kernel parameters; returns SA_OK or an error (message set).
 int resolve(const sa_attn_args* a, sa::AttnParams* p) {
   if (a == nullptr) return fail(SA_ERR_INVALID, "args is NULL");
@@ -88,6 +93,10 @@ int resolve(const sa_attn_args* a, sa::AttnParams* p) {
                 (long long)HD, (long long)a->ldq, (long long)a->ldk, (long long)a->ldv, (long long)ldo);
   if (a->B > 1 && (a->sq < 0 || a->sk < 0 || a->sv < 0 || a->so < 0))
     return fail(SA_ERR_INVALID, "batch strides must be >= 0");
+  if (too_large(a->q_off) || too_large(a->k_off) || too_large(a->v_off) || too_large(a->o_off) ||
+      too_large(a->ldq) || too_large(a->ldk) || too_large(a->ldv) || too_large(ldo) || too_large(a->sq) ||
+      too_large(a->sk) || too_large(a->sv) || too_large(a->so) || too_large(a->sbias) || too_large(a->smask))
+    return fail(SA_ERR_INVALID, "offsets and strides must be below 2^40 elements");
   const int64_t so = a->B > 1 ? a->so : 0;
   if (a->B > 1 && so < (int64_t)(a->Lq - 1) * ldo + HD)
     return fail(SA_ERR_INVALID, "output batch stride %lld makes sequences overlap", (long long)so);
@@ -179,6 +188,9 @@ int resolve_linear(const sa_linear_args* a, sa::LinearParams* p) {
     return fail(SA_ERR_INVALID, "row strides of x and w must be >= K = %d (ldx=%lld ldw=%lld)", a->K, (long long)ldx,
                 (long long)ldw);
   if (ldy < a->N) return fail(SA_ERR_INVALID, "row stride of y must be >= N = %d (ldy=%lld)", a->N, (long long)ldy);
+  if (too_large(a->x_off) || too_large(a->y_off) || too_large(a->gate_off) || too_large(ldx) || too_large(ldw) ||
+      too_large(ldy))
+    return fail(SA_ERR_INVALID, "offsets and strides must be below 2^40 elements");
   if (!isfinite(a->alpha)) return fail(SA_ERR_INVALID, "alpha must be finite");
   if (a->act < SA_ACT_NONE || a->act > SA_ACT_SILU) return fail(SA_ERR_INVALID, "unknown act %d", a->act);
   if (a->epilogue < SA_EPI_STORE || a->epilogue > SA_EPI_RESID_GATE)

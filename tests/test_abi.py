@@ -128,6 +128,9 @@ def test_generic_kernel_for_other_head_dims_and_unaligned_rows():
     (dict(ldo=100), _lib.SA_ERR_INVALID),
     (dict(so=100), _lib.SA_ERR_INVALID),
     (dict(sq=-1), _lib.SA_ERR_INVALID),
+    (dict(k_off=1 << 40), _lib.SA_ERR_INVALID),
+    (dict(ldv=1 << 41), _lib.SA_ERR_INVALID),
+    (dict(sk=1 << 40), _lib.SA_ERR_INVALID),
     (dict(o=FAKE + 4096), _lib.SA_ERR_ALIAS),
     (dict(bias_mode=1), _lib.SA_ERR_INVALID),
     (dict(bias_mode=2, bias=FAKE + (2 << 32)), _lib.SA_ERR_INVALID),
@@ -264,6 +267,8 @@ def test_linear_kernel_choice():
     (dict(ldw=100), _lib.SA_ERR_INVALID),
     (dict(ldy=100), _lib.SA_ERR_INVALID),
     (dict(x_off=-4), _lib.SA_ERR_INVALID),
+    (dict(y_off=1 << 40), _lib.SA_ERR_INVALID),
+    (dict(ldw=1 << 40), _lib.SA_ERR_INVALID),
     (dict(alpha=float("nan")), _lib.SA_ERR_INVALID),
     (dict(act=9), _lib.SA_ERR_INVALID),
     (dict(epilogue=3), _lib.SA_ERR_INVALID),
