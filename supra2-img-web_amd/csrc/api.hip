@@ -10,6 +10,7 @@
 #include <math.h>
 #include <atomic>
 #include <stdarg.h>
+#include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -54,14 +55,23 @@ using sa::fail;
 using sa::hip_fail;
 using sa::ok;
 
-// Byte extent [lo, hi) touched by a strided [B, L, H*D] view of `base`.
+// Byte extent [lo, hi) touched by a strided [B, L, H*D] view of `base`; ok is false when the
+// arithmetic overflows (then lo and hi mean nothing).
 struct Extent {
   uintptr_t lo, hi;
+  bool ok;
 };
 
 Extent extent(const void* base, int64_t off, int64_t sb, int64_t ld, int B, int L, int64_t row) {
-  const int64_t last = off + (B > 1 ? (int64_t)(B - 1) * sb : 0) + (int64_t)(L - 1) * ld + row;
-  return {(uintptr_t)base + (uintptr_t)(off * 4), (uintptr_t)base + (uintptr_t)(last * 4)};
+  int64_t last = off, t = 0;
+  bool ok = true;
+  if (B > 1) ok = !__builtin_mul_overflow((int64_t)(B - 1), sb, &t) && !__builtin_add_overflow(last, t, &last);
+  if (ok && L > 1) ok = !__builtin_mul_overflow((int64_t)(L - 1), ld, &t) && !__builtin_add_overflow(last, t, &last);
+  ok = ok && !__builtin_add_overflow(last, row, &last) && last >= 0 && last <= INT64_MAX / 4;
+  uintptr_t lo = 0, hi = 0;
+  ok = ok && !__builtin_add_overflow((uintptr_t)base, (uintptr_t)off * 4, &lo) &&
+       !__builtin_add_overflow((uintptr_t)base, (uintptr_t)last * 4, &hi);
+  return {lo, hi, ok};
 }
 
 bool overlaps(const Extent& a, const Extent& b) { return a.lo < b.hi && b.lo < a.hi; }
@@ -107,6 +117,8 @@ int resolve(const sa_attn_args* a, sa::AttnParams* p) {
   const Extent eq = extent(a->q, a->q_off, a->sq, a->ldq, a->B, a->Lq, HD);
   const Extent ek = extent(a->k, a->k_off, a->sk, a->ldk, a->B, a->Lk, HD);
   const Extent ev = extent(a->v, a->v_off, a->sv, a->ldv, a->B, a->Lk, HD);
+  if (!eo.ok || !eq.ok || !ek.ok || !ev.ok)
+    return fail(SA_ERR_INVALID, "the extent of q, k, v or o overflows 64-bit addresses");
   if (overlaps(eo, eq) || overlaps(eo, ek) || overlaps(eo, ev))
     return fail(SA_ERR_ALIAS, "the output overlaps q, k or v");
 
@@ -198,8 +210,10 @@ int resolve_linear(const sa_linear_args* a, sa::LinearParams* p) {
   if (a->epilogue == SA_EPI_RESID_GATE && !a->gate) return fail(SA_ERR_INVALID, "SA_EPI_RESID_GATE needs gate");
   // the output must not overlap what the kernel reads (it reads y itself only at the element it writes)
   const Extent ey = extent(a->y, a->y_off, 0, ldy, 1, a->M, a->N);
-  if (overlaps(ey, extent(a->x, a->x_off, 0, ldx, 1, a->M, a->K)) || overlaps(ey, extent(a->w, 0, 0, ldw, 1, a->N, a->K)))
-    return fail(SA_ERR_ALIAS, "y overlaps x or w");
+  const Extent ex = extent(a->x, a->x_off, 0, ldx, 1, a->M, a->K);
+  const Extent ew = extent(a->w, 0, 0, ldw, 1, a->N, a->K);
+  if (!ey.ok || !ex.ok || !ew.ok) return fail(SA_ERR_INVALID, "the extent of x, w or y overflows 64-bit addresses");
+  if (overlaps(ey, ex) || overlaps(ey, ew)) return fail(SA_ERR_ALIAS, "y overlaps x or w");
   if (a->bias && overlaps(ey, extent(a->bias, 0, 0, 0, 1, 1, a->N))) return fail(SA_ERR_ALIAS, "y overlaps bias");
   if (a->epilogue == SA_EPI_RESID_GATE && overlaps(ey, extent(a->gate, a->gate_off, 0, 0, 1, 1, a->N)))
     return fail(SA_ERR_ALIAS, "y overlaps gate");
@@ -330,7 +344,7 @@ int sa_attention_f32(const sa_attn_args* args, void* stream) {
         return fail(SA_ERR_INVALID, "this call needs a device workspace of %lld bytes (sa_attention_workspace_bytes)",
                     (long long)need);
       if (!aligned16(args->workspace)) return fail(SA_ERR_INVALID, "workspace must be 16-byte aligned");
-      const Extent ew = {(uintptr_t)args->workspace, (uintptr_t)args->workspace + (uintptr_t)need};
+      const Extent ew = {(uintptr_t)args->workspace, (uintptr_t)args->workspace + (uintptr_t)need, true};
       const int64_t HD = (int64_t)p.H * p.D;
       if (overlaps(ew, extent(p.o, p.o_off, p.so, p.ldo, p.B, p.Lq, HD)) ||
           overlaps(ew, extent(p.q, p.q_off, p.sq, p.ldq, p.B, p.Lq, HD)) ||
@@ -388,9 +402,9 @@ int sa_vae_attention_f32(const sa_vae_attn_args* a, void* stream) {
   if (!aligned16(a->workspace)) return fail(SA_ERR_INVALID, "workspace must be 16-byte aligned");
   const int64_t HW = a->HW, C = a->C;
   auto span = [](const void* p, int64_t floats) -> Extent {
-    return {(uintptr_t)p, (uintptr_t)p + (uintptr_t)(floats * 4)};
+    return {(uintptr_t)p, (uintptr_t)p + (uintptr_t)(floats * 4), true};
   };
-  const Extent ew = {(uintptr_t)a->workspace, (uintptr_t)a->workspace + (uintptr_t)L.total};
+  const Extent ew = {(uintptr_t)a->workspace, (uintptr_t)a->workspace + (uintptr_t)L.total, true};
   const Extent ex = span(a->x, HW * C), eo = span(a->out, HW * C);
   if (overlaps(ew, ex) || overlaps(ew, eo)) return fail(SA_ERR_ALIAS, "the workspace overlaps x or out");
   if (a->out != a->x && overlaps(eo, ex)) return fail(SA_ERR_ALIAS, "out overlaps x (pass out == x to update in place)");

@@ -196,7 +196,50 @@ var forms = {
   },
 };
 
+// The addon's buffer validation (what WebGPU checks for bindings and writeBuffer): every range a call
+// touches must lie inside its buffer, released handles throw, overlapping copies are refused. Each
+// of these throws before any device work, so nothing out of range reaches the GPU.
+function boundaryChecks(gpu) {
+  var n = gpu.native;
+  var assert = require("assert");
+  var code = function (c, re) {
+    return function (e) { return e.code === c && re.test(e.message); };
+  };
+  var buf = n.malloc(256);
+  var other = n.malloc(1024);
+  n.upload(buf, new Float32Array(64), 0);                       // exactly fills it
+  assert.throws(function () { n.upload(buf, new Float32Array(64), 4); }, code("SA_ERR_INVALID", /outside the 256-byte buffer/));
+  assert.throws(function () { n.download(buf, new Float32Array(65), 0); }, code("SA_ERR_INVALID", /outside/));
+  assert.throws(function () { n.memset(buf, 0, 257); }, code("SA_ERR_INVALID", /outside/));
+  assert.throws(function () { n.copy(other, 0, buf, 128, 256); }, code("SA_ERR_INVALID", /copy src/));
+  assert.throws(function () { n.copy(other, 0, other, 64, 128); }, code("SA_ERR_ALIAS", /overlap/));
+  n.copy(other, 512, other, 0, 256);                            // disjoint ranges of one buffer are fine
+  // Calls whose operand extent runs 8 bytes past its buffer (allocations are at least 256-byte
+  // aligned, so the claimed range cannot reach another allocation and only the bounds check fires):
+  // attention with q of 4 rows x 64 floats (1024 bytes) in a 1016-byte buffer
+  var qb = n.malloc(1016), kv = n.malloc(1024), ob = n.malloc(1024);
+  assert.throws(function () {
+    n.attention({ B: 1, H: 1, D: 64, Lq: 4, Lk: 4, q: qb, k: kv, v: kv, out: ob, ldq: 64, ldk: 64, ldv: 64, scale: 1 });
+  }, code("SA_ERR_INVALID", /^q: 1024 bytes at byte offset 0 lie outside the 1016-byte buffer/));
+  // linear with y of 2 x 64 floats (512 bytes) in a 504-byte buffer, then x of 2 x 8 floats in 56 bytes
+  var lx = n.malloc(64), lw = n.malloc(2048), ly = n.malloc(504), lx2 = n.malloc(56);
+  assert.throws(function () { n.linear({ M: 2, N: 64, K: 8, x: lx, w: lw, y: ly }); },
+    code("SA_ERR_INVALID", /^y: 512 bytes at byte offset 0 lie outside the 504-byte buffer/));
+  assert.throws(function () { n.linear({ M: 2, N: 64, K: 8, x: lx2, w: lw, y: ob }); },
+    code("SA_ERR_INVALID", /^x: 64 bytes at byte offset 0 lie outside the 56-byte buffer/));
+  [qb, kv, ob, lx, lw, ly, lx2].forEach(function (b) { n.free(b); });
+  var ev = n.eventCreate();
+  n.eventDestroy(ev);
+  assert.throws(function () { n.eventRecord(ev); }, code("SA_ERR_INVALID", /has been released/));
+  n.free(buf);
+  assert.throws(function () { n.free(buf); }, code("SA_ERR_INVALID", /has been released/));
+  assert.throws(function () { n.upload(buf, new Float32Array(4), 0); }, code("SA_ERR_INVALID", /has been released/));
+  n.free(other);
+  process.stdout.write("node: boundary checks passed\n");
+}
+
 sa.GPU.create().then(function (gpu) {
+  boundaryChecks(gpu);
   var chain = Promise.resolve();
   manifest.cases.forEach(function (c) {
     chain = chain.then(function () {

@@ -31,6 +31,33 @@ check("addon exports", function () {
   assert.strictEqual(native.SA_MASK_KEY_MASK, 2);
 });
 
+check("handles: only this addon's, of the right kind, and live", function () {
+  var invalid = function (re) {
+    return function (e) { return e.code === "SA_ERR_INVALID" && re.test(e.message); };
+  };
+  // not a handle at all: plain objects, numbers, typed arrays
+  assert.throws(function () { native.upload({}, new Float32Array(4), 0); }, invalid(/buffer must be a device buffer handle/));
+  assert.throws(function () { native.free(12345); }, invalid(/buffer must be a device buffer handle/));
+  assert.throws(function () { native.copy(new Float32Array(4), 0, null, 0, 16); }, invalid(/dst must be a device buffer/));
+  assert.throws(function () {
+    native.attention({ B: 1, H: 1, D: 64, Lq: 4, Lk: 4, q: { buf: 1 }, ldq: 64, ldk: 64, ldv: 64 });
+  }, invalid(/q must be a device buffer handle/));
+  assert.throws(function () { native.eventRecord({}); }, invalid(/event must be an event handle/));
+  // a handle of another kind: an opened file where a device buffer or an event belongs
+  var bytes = fs.readFileSync(JSON.parse(fs.readFileSync(process.argv[3], "utf8")).file);
+  var f = native.stOpenBytes(new Uint8Array(bytes.buffer, bytes.byteOffset, bytes.length));
+  assert.throws(function () { native.upload(f, new Float32Array(4), 0); }, invalid(/device buffer handle/));
+  assert.throws(function () { native.linear({ M: 1, N: 1, K: 8, x: f }); }, invalid(/x must be a device buffer handle/));
+  assert.throws(function () { native.eventDestroy(f); }, invalid(/event handle/));
+  assert.throws(function () { native.freeHost(f); }, invalid(/pinned host buffer handle/));
+  assert.ok(native.stNames(f).length > 0);
+  // released: a closed file throws on use, closing again is allowed
+  native.stClose(f);
+  assert.throws(function () { native.stNames(f); }, invalid(/has been released/));
+  native.stClose(f);
+  assert.throws(function () { native.stClose({}); }, invalid(/safetensors handle/));
+});
+
 check("bucket LUT matches the oracle's", function () {
   var expected = JSON.parse(fs.readFileSync(process.argv[2], "utf8"));
   var lut = native.bucketLut(expected.Lq, expected.Lk, 32, 128, true);

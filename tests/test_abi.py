@@ -152,6 +152,19 @@ def test_invalid_calls_are_rejected_before_launch(over, code):
     assert _lib.load().sa_attention_kernel_name(ctypes.byref(args)) is None
 
 
+def test_extents_that_overflow_are_rejected():
+    """Offsets and strides below the 2^40 limit can still multiply past int64 with a large batch or
+    row count: the extent arithmetic is checked, and such calls fail with a message that says so."""
+    lib = _lib.load()
+    big = (1 << 40) - 1
+    args = good_args(B=1 << 30, sq=big, sk=big, sv=big, so=big)
+    assert rc_of(args) == _lib.SA_ERR_INVALID
+    assert b"overflows" in lib.sa_last_error()
+    largs = lin_args(M=(1 << 31) - 1, ldx=big, ldy=big)
+    assert lib.sa_linear_f32(ctypes.byref(largs), None) == _lib.SA_ERR_INVALID
+    assert b"overflows" in lib.sa_last_error()
+
+
 def test_null_args_pointer():
     lib = _lib.load()
     assert lib.sa_attention_f32(None, None) == _lib.SA_ERR_INVALID
@@ -241,7 +254,7 @@ def lin_args(**over):
 
 
 def test_linear_kernel_choice():
-    # DiT layers at batch 64 (16384 rows): 128 x 192 tiles for wide outputs, 64 x 64 for 576-wide ones
+    # DiT layers at batch 64 (16384 rows): 64 x 192 or 128 x 192 tiles while the grid fills the chip, else 64 x 64
     assert _lib.linear_kernel_name(lin_args(M=16384, N=1728, K=576)) == "linear_mfma_64x192"       # qkv
     assert _lib.linear_kernel_name(lin_args(M=16384, N=2304, K=576)) == "linear_mfma_128x192"      # fc1
     assert _lib.linear_kernel_name(lin_args(M=16384, N=576, K=576)) == "linear_mfma_64x192_bk16"   # proj, q, cproj

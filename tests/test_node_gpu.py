@@ -146,6 +146,7 @@ def test_reference_call_forms_through_node(tmp_path):
                          text=True, timeout=300)
     print(res.stdout, res.stderr, flush=True)
     assert res.returncode == 0, res.stderr
+    assert "node: boundary checks passed" in res.stdout
     for case in cases:
         got = np.fromfile(os.path.join(d, case["name"] + ".out.bin"), dtype=np.float32)
         ref = refs[case["name"]]
