@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SA_ABI_VERSION 2
+#define SA_ABI_VERSION 3
 
 /* ---- status codes ---- */
 #define SA_OK 0
@@ -74,7 +74,8 @@ extern "C" {
  * are all masked produces zeros (the F.scaled_dot_product_attention convention).
  *
  * Set struct_size = sizeof(sa_attn_args) (checked, so that later ABI revisions can grow the
- * struct). Zero-initialise unused fields.
+ * struct; the revision-2 size, which ends at workspace_bytes, is still accepted). Zero-initialise
+ * unused fields.
  */
 typedef struct sa_attn_args {
   uint32_t struct_size;
@@ -102,6 +103,12 @@ typedef struct sa_attn_args {
   int64_t smask;                      /* KEY_MASK batch stride (bytes = elements); <= 0 means Lk */
   void* workspace;                    /* device scratch, 16-byte aligned, when the call needs it */
   int64_t workspace_bytes;            /* its size (>= sa_attention_workspace_bytes(args)) */
+  /* Revision 3. KEY_LEN: an optional HOST copy of key_len[0..B), read during the call and used
+   * only to schedule the sequences longest first (balanced over the device's L2 domains) when
+   * 8 <= B <= 256; the results come from the device key_len either way, so a stale copy costs
+   * speed, never correctness. The DiT caller knows its prompt lengths on the host
+   * (app/models/dit.js:137-144). */
+  const int32_t* key_len_host;
 } sa_attn_args;
 
 /* Fused attention, fp32 in and out, fp32 MFMA arithmetic. Replaces ops.attention

@@ -8,7 +8,9 @@
 #include <hip/hip_runtime.h>
 
 #include <math.h>
+#include <algorithm>
 #include <atomic>
+#include <stddef.h>
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -83,12 +85,35 @@ bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 constexpr int64_t kMaxExtent = (int64_t)1 << 40;
 bool too_large(int64_t v) { return v >= kMaxExtent; }
 
+// Size of the revision-2 struct (it ended at workspace_bytes); still accepted.
+constexpr uint32_t kAttnArgsV2Size = offsetof(sa_attn_args, key_len_host);
+
+// Longest-first schedule for per-sequence key lengths known on the host: sequences sorted by key
+// blocks, longest first (stable), then dealt round-robin over the 8 L2 domains when B is a
+// multiple of 8. The flash grid's workgroup remap gives domain x the sequence ranks
+// [x*B/8, (x+1)*B/8) in launch order, so every domain gets an even share of the long sequences and
+// starts its own longest first; the short ones fill the tail. Allocation-free (B <= kMaxOrder).
+void longest_first(const int32_t* len, int B, int Lk, uint8_t* order) {
+  int idx[sa::kMaxOrder], nb[sa::kMaxOrder];
+  for (int i = 0; i < B; ++i) {
+    nb[i] = (std::min(std::max(len[i], 0), Lk) + 31) / 32;
+    int j = i;
+    for (; j > 0 && nb[idx[j - 1]] < nb[i]; --j) idx[j] = idx[j - 1];  // insertion sort, stable
+    idx[j] = i;
+  }
+  for (int j = 0; j < B; ++j) {
+    const int rank = B % 8 == 0 ? (j % 8) * (B / 8) + j / 8 : j;
+    order[rank] = (uint8_t)idx[j];
+  }
+}
+
 // Resolves an sa_attn_args into kernel parameters; returns SA_OK or an error (message set).
 int resolve(const sa_attn_args* a, sa::AttnParams* p) {
   if (a == nullptr) return fail(SA_ERR_INVALID, "args is NULL");
-  if (a->struct_size != sizeof(sa_attn_args))
+  if (a->struct_size != sizeof(sa_attn_args) && a->struct_size != kAttnArgsV2Size)
     return fail(SA_ERR_INVALID, "struct_size %u does not match sizeof(sa_attn_args) = %zu", a->struct_size,
                 sizeof(sa_attn_args));
+  const int32_t* key_len_host = a->struct_size >= sizeof(sa_attn_args) ? a->key_len_host : nullptr;
   if (a->B < 1 || a->H < 1 || a->D < 1 || a->Lq < 1 || a->Lk < 1)
     return fail(SA_ERR_INVALID, "B, H, D, Lq, Lk must be >= 1 (got B=%d H=%d D=%d Lq=%d Lk=%d)", a->B, a->H, a->D,
                 a->Lq, a->Lk);
@@ -182,6 +207,18 @@ int resolve(const sa_attn_args* a, sa::AttnParams* p) {
   p->key_len = a->key_len;
   p->key_mask = a->key_mask;
   p->smask = a->B > 1 ? (a->smask > 0 ? a->smask : a->Lk) : 0;
+  // The schedule pays one dependent kernel-argument load per workgroup: used only when the batch
+  // is large enough to queue workgroups (small batches run in one round) and the order is not the
+  // launch order already.
+  p->order_n = 0;
+  if (a->mask_mode == SA_MASK_KEY_LEN && key_len_host && a->B >= 8 && a->B <= sa::kMaxOrder) {
+    longest_first(key_len_host, a->B, a->Lk, p->order);
+    for (int r = 0; r < a->B; ++r)
+      if (p->order[r] != r) {
+        p->order_n = a->B;
+        break;
+      }
+  }
   return SA_OK;
 }
 

@@ -111,13 +111,14 @@ __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void
   const int qtile = tile % q_tiles;
   tile /= q_tiles;
   const int h = tile % p.H;
-  const int b = tile / p.H;
+  int b = tile / p.H;
+  if constexpr (MASK == MASK_KEY_LEN_ORDERED) b = p.order[b];  // the longest-first schedule
   const int q0 = qtile * QT;
   const int qi = q0 + qg * 32 + col;
   const bool q_valid = qi < p.Lq;
 
   int kv_len = p.Lk;
-  if constexpr (MASK == MASK_KEY_LEN) kv_len = min(max(p.key_len[b], 0), p.Lk);
+  if constexpr (MASK == MASK_KEY_LEN || MASK == MASK_KEY_LEN_ORDERED) kv_len = min(max(p.key_len[b], 0), p.Lk);
   const int nblk = (kv_len + 31) >> 5;
   const int nstep = (nblk + NSPLIT - 1) / NSPLIT;
   constexpr bool use_kmask = MASK == MASK_KEY_MASK;
@@ -460,7 +461,9 @@ template <int D, int NSPLIT, int BIAS>
 hipError_t launch_mask(const AttnParams& p, int q_tiles, dim3 grid, int num_cus, hipStream_t stream) {
   switch (p.mask_mode) {
     case MASK_NONE: return launch_one<D, NSPLIT, BIAS, MASK_NONE>(p, q_tiles, grid, num_cus, stream);
-    case MASK_KEY_LEN: return launch_one<D, NSPLIT, BIAS, MASK_KEY_LEN>(p, q_tiles, grid, num_cus, stream);
+    case MASK_KEY_LEN:
+      if (p.order_n > 0) return launch_one<D, NSPLIT, BIAS, MASK_KEY_LEN_ORDERED>(p, q_tiles, grid, num_cus, stream);
+      return launch_one<D, NSPLIT, BIAS, MASK_KEY_LEN>(p, q_tiles, grid, num_cus, stream);
     case MASK_KEY_MASK: return launch_one<D, NSPLIT, BIAS, MASK_KEY_MASK>(p, q_tiles, grid, num_cus, stream);
     default: return hipErrorInvalidValue;
   }

@@ -7,6 +7,8 @@
 namespace sa {
 
 // Everything a kernel needs for one attention call, resolved and validated by the host.
+constexpr int kMaxOrder = 256;  // sequences a launch schedule can order (kernel-argument bytes)
+
 struct AttnParams {
   const float* q;
   const float* k;
@@ -26,10 +28,18 @@ struct AttnParams {
   const int32_t* key_len;
   const uint8_t* key_mask;
   int64_t smask;
+  // Sequence schedule of the flash kernel: sequence rank r (its position in the launch order)
+  // runs sequence order[r] when order_n > 0, sequence r otherwise. Kernel-argument data, so the
+  // lookup is a scalar load and needs no device allocation.
+  int order_n;
+  uint8_t order[kMaxOrder];
 };
 
 enum { BIAS_NONE = 0, BIAS_DENSE = 1, BIAS_RELPOS = 2 };
 enum { MASK_NONE = 0, MASK_KEY_LEN = 1, MASK_KEY_MASK = 2 };
+// Flash-kernel variant only (never an ABI value): key lengths plus the sequence schedule in
+// AttnParams::order, so that the plain key-length variant does not read the schedule at all.
+constexpr int MASK_KEY_LEN_ORDERED = 3;
 
 // Flash kernel on fp32 MFMA for D in {64, 128} with 16-byte aligned rows.
 // nsplit in {1, 2, 4}: key blocks are split across the 4 waves of a workgroup. num_cus (the

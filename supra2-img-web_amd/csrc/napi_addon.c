@@ -286,8 +286,8 @@ static int prop_buf(napi_env env, napi_value obj, const char* name, Handle** out
 
 /* opts -> sa_attn_args. Field names are those of app/gpu/ops.js:109 (q, k, v, Lq, Lk, H, D, ldq,
  * ldk, ldv, qOff, kOff, vOff, oOff, scale) plus out -> o, and the extension fields B, ldo, sq, sk,
- * sv, so, biasMode, bias, sbias, bucketLut, numBuckets, maskMode, keyLen, keyMask, smask,
- * workspace, workspaceBytes. */
+ * sv, so, biasMode, bias, sbias, bucketLut, numBuckets, maskMode, keyLen, keyLenHost, keyMask,
+ * smask, workspace, workspaceBytes. */
 typedef struct AttnHandles {
   Handle *q, *k, *v, *out, *bias, *lut, *kl, *km, *ws;
 } AttnHandles;
@@ -318,6 +318,23 @@ static int fill_args(napi_env env, napi_value o, sa_attn_args* a, AttnHandles* h
       prop_i64(env, o, "workspaceBytes", 0, &a->workspace_bytes))
     return 1;
   if (prop(env, o, "scale", &sv) || get_f64(env, sv, 1.0, &scale, "scale")) return 1;
+  /* keyLenHost: optional Int32Array host copy of keyLen (>= B entries), read during the call */
+  napi_value klh;
+  if (prop(env, o, "keyLenHost", &klh)) return 1;
+  if (!is_nullish(env, klh)) {
+    bool is_ta = false;
+    napi_typedarray_type type;
+    size_t length = 0, offset = 0;
+    void* data = NULL;
+    napi_value ab;
+    if (napi_is_typedarray(env, klh, &is_ta) != napi_ok || !is_ta ||
+        napi_get_typedarray_info(env, klh, &type, &length, &data, &ab, &offset) != napi_ok || type != napi_int32_array ||
+        B < 1 || (int64_t)length < B) {
+      napi_throw_type_error(env, "SA_ERR_INVALID", "keyLenHost must be an Int32Array of at least B lengths");
+      return 1;
+    }
+    a->key_len_host = (const int32_t*)data;
+  }
   if (B < -0x7fffffffLL || B > 0x7fffffffLL || H > 0x7fffffffLL || D > 0x7fffffffLL || Lq > 0x7fffffffLL ||
       Lk > 0x7fffffffLL) {
     napi_throw_range_error(env, "SA_ERR_INVALID", "sizes must fit in int32");

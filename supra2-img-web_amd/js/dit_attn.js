@@ -11,7 +11,7 @@
 // so the result equals the per-sample call at its true length).
 //
 //   selfAttention(gpu, qkv, B, opts)     -> Tensor [B*T, dim]
-//   packContexts(gpu, kvs, lens, opts)   -> { kv, keyLen, Lmax, B, release() }
+//   packContexts(gpu, kvs, lens, opts)   -> { kv, keyLen, lens, Lmax, B, release() }
 //   crossAttention(gpu, q, ctx, opts)    -> Tensor [B*T, dim]
 // opts: { tokens = 256, dim = 576, heads = 9, out } (the DiT config of app/models/dit.js).
 "use strict";
@@ -60,9 +60,10 @@ function packContexts(gpu, kvs, lens, opts) {
     }
     gpu.native.copy(kv.buf, b * Lmax * row, kvs[b].buf, 0, lens[b] * row);
   }
-  var keyLen = gpu.fromArray(Int32Array.from(lens), [B]);
+  var hostLens = Int32Array.from(lens);
+  var keyLen = gpu.fromArray(hostLens, [B]);
   return {
-    kv: kv, keyLen: keyLen, Lmax: Lmax, B: B,
+    kv: kv, keyLen: keyLen, lens: hostLens, Lmax: Lmax, B: B,
     release: function () { kv.release(); keyLen.release(); },
   };
 }
@@ -74,7 +75,7 @@ function crossAttention(gpu, q, ctx, opts) {
   return ops.attention(gpu, {
     B: ctx.B, q: q, k: ctx.kv, v: ctx.kv, Lq: c.T, Lk: ctx.Lmax, H: c.H, D: c.D, ldq: c.dim, ldk: ldkv, ldv: ldkv,
     qOff: 0, kOff: 0, vOff: c.dim, sq: c.T * c.dim, sk: ctx.Lmax * ldkv, sv: ctx.Lmax * ldkv, so: c.T * c.dim,
-    keyLen: ctx.keyLen, out: c.out,
+    keyLen: ctx.keyLen, keyLenHost: ctx.lens, out: c.out,  // host lengths: longest-first schedule
   });
 }
 

@@ -140,6 +140,7 @@ class AttnArgs(ctypes.Structure):
         ("smask", c_int64),
         ("workspace", c_void_p),
         ("workspace_bytes", c_int64),
+        ("key_len_host", c_void_p),  # revision 3: host copy of key_len, schedules longest first
     ]
 
     def __init__(self, **kw):

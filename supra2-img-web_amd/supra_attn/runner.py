@@ -10,12 +10,17 @@ from .workloads import Call
 
 
 class Staged:
-    """Device-resident buffers of one call plus its ready-to-launch sa_attn_args."""
+    """Device-resident buffers of one call plus its ready-to-launch sa_attn_args.
 
-    def __init__(self, dev: Device, call: Call, out_fill: float | None = None):
+    With per-sequence key lengths, the host copy of the lengths goes along too (key_len_host), so
+    the library schedules the sequences longest first, as the DiT caller does; host_key_len=False
+    leaves it out (the launch-order schedule)."""
+
+    def __init__(self, dev: Device, call: Call, out_fill: float | None = None, host_key_len: bool = True):
         self.dev = dev
         self.call = call
         self.bufs = []
+        self.key_len_host = None
         q = self._put(call.q)
         k = q if call.same_qkv else self._put(call.k)
         v = q if call.same_qkv else (k if call.v is call.k else self._put(call.v))
@@ -33,7 +38,11 @@ class Staged:
             kw["bucket_lut"] = self._put(np.asarray(call.lut, dtype=np.int32)).ptr
             kw["num_buckets"] = int(call.bias.shape[0])
         if call.key_len is not None:
-            kw["key_len"] = self._put(np.asarray(call.key_len, dtype=np.int32)).ptr
+            kl = np.ascontiguousarray(call.key_len, dtype=np.int32)
+            kw["key_len"] = self._put(kl).ptr
+            if host_key_len:
+                self.key_len_host = kl  # kept alive: the library reads it during each call
+                kw["key_len_host"] = kl.ctypes.data
         if call.key_mask is not None:
             km = np.asarray(call.key_mask, dtype=np.uint8)
             kw["key_mask"] = self._put(km).ptr

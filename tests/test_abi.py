@@ -40,7 +40,7 @@ def test_every_declared_symbol_is_exported_and_bound():
 
 def test_version_and_constants():
     lib = _lib.load()
-    assert lib.sa_version() == 2
+    assert lib.sa_version() == 3
     text = open(HEADER).read()
     text += open(os.path.join(ROOT, "include", "supra_linear.h")).read()
     weights = open(os.path.join(ROOT, "include", "supra_weights.h")).read()
@@ -149,6 +149,22 @@ def test_invalid_calls_are_rejected_before_launch(over, code):
     assert rc_of(args) == code
     msg = _lib.load().sa_last_error().decode()
     assert msg, "an error must carry a message"
+    assert _lib.load().sa_attention_kernel_name(ctypes.byref(args)) is None
+
+
+def test_revision2_struct_size_is_accepted():
+    """Callers built against revision 2 (the struct ending at workspace_bytes) keep working; the
+    revision-3 field (key_len_host) is then treated as absent."""
+    v2 = _lib.AttnArgs.key_len_host.offset
+    assert v2 + ctypes.sizeof(ctypes.c_void_p) == ctypes.sizeof(_lib.AttnArgs)
+    for over in (dict(), dict(mask_mode=_lib.SA_MASK_KEY_LEN, key_len=FAKE + (5 << 32))):
+        args = good_args(**over)
+        full = _lib.kernel_name(args)
+        args.struct_size = v2
+        args.key_len_host = 1  # past the revision-2 struct: must not be read
+        assert _lib.kernel_name(args) == full
+    args = good_args()
+    args.struct_size = v2 + 4
     assert _lib.load().sa_attention_kernel_name(ctypes.byref(args)) is None
 
 

@@ -1,0 +1,58 @@
+"""The longest-first sequence schedule (sa_attn_args.key_len_host, GPU).
+
+A host copy of the per-sequence key lengths lets the library launch the longest sequences first,
+balanced over the L2 domains. It changes only which workgroup runs which sequence, so the output
+must be bit-identical with the host copy, without it, and with a stale (wrong) host copy - the
+kernel reads the device key lengths for the arithmetic - and must match the oracle at the usual
+bar. Cases: the sweep's batch-64 cross-attention (round-robin over the domains), batch 24 (also a
+multiple of 8), batch 13 (plain longest-first order) and batch 2 (below the batch the schedule is
+used for, so all three runs take the launch order)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import attention as orc
+from supra_attn import _lib, workloads
+from supra_attn.runner import Staged
+from cases import make_call
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+def _calls():
+    yield "sweep_cross_b64", workloads.SweepData(blocks=1).block(0)[1]
+    for B, seed in ((24, 31), (13, 32), (2, 33)):
+        rng = np.random.default_rng(seed)
+        key_len = [int(x) for x in rng.integers(0, 129, size=B)]  # zero-length sequences included
+        key_len[0] = 128
+        yield f"B{B}", make_call(B=B, H=9, D=64, Lq=256, Lk=128, seed=seed, mask_mode=_lib.SA_MASK_KEY_LEN,
+                                 key_len=key_len)
+
+
+CALLS = list(_calls())
+
+
+@pytest.mark.parametrize("name,call", CALLS, ids=[c[0] for c in CALLS])
+def test_schedule_is_bitwise_neutral(dev, name, call):
+    print(f"[schedule case] {name} B={call.B} kernel=", end="", flush=True)
+    outs = {}
+    for mode in ("host", "none", "stale"):
+        st = Staged(dev, call, out_fill=np.nan, host_key_len=mode != "none")
+        try:
+            if mode == "stale":  # a wrong host copy: reversed lengths, so the order is wrong too
+                st.key_len_host = np.ascontiguousarray(st.key_len_host[::-1])
+                st.args.key_len_host = st.key_len_host.ctypes.data
+            if mode == "host":
+                print(st.kernel, flush=True)
+            outs[mode] = st.run()
+        finally:
+            st.release()
+    for mode in ("none", "stale"):
+        np.testing.assert_array_equal(outs[mode].view(np.uint32), outs["host"].view(np.uint32), err_msg=mode)
+    ref = orc.reference_torch(call)
+    e = orc.errors(orc.output_view(outs["host"], call), ref)
+    assert e["finite"] and e["rel_l2"] <= TOL and e["max_rel"] <= TOL, e
