@@ -84,6 +84,14 @@ check("invalid calls throw with a status code before touching the device", funct
   }, function (e) {
     return e.code === "SA_ERR_INVALID";
   });
+  // the host copy of the key lengths must be an Int32Array of at least B entries (it is read on the host)
+  [[77, 1], new Float32Array(2), new Int32Array(1)].forEach(function (klh) {
+    assert.throws(function () {
+      native.attention({ B: 2, H: 9, D: 64, Lq: 256, Lk: 128, ldq: 576, ldk: 1152, ldv: 1152, keyLenHost: klh });
+    }, function (e) {
+      return e.code === "SA_ERR_INVALID" && /keyLenHost must be an Int32Array of at least B lengths/.test(e.message);
+    });
+  });
 });
 
 // a fake addon: records calls, hands out numbered buffers
