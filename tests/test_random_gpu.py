@@ -6,9 +6,10 @@ The draws are seeded, so the cases are the same on every run. Attention calls co
 (flash MFMA at head dims 64/128 with and without key splits, the wide-head kernel at 256/512, the
 generic kernel at other head dims and unaligned rows), packed and separate q/k/v, padded rows,
 element offsets, output row padding, scales of either sign, dense and relative-position biases,
-per-sequence key lengths (zero included) and boolean key masks. Linear calls cover both MFMA tiles
-and the generic kernel, ragged M/N/K, strides and offsets on every operand, alpha, the four
-activations and the three epilogues. Sizes keep the float64 oracle to a few seconds in total.
+per-sequence key lengths (zero included) and boolean key masks. Linear calls cover the 64 x 64 MFMA
+tile and the generic kernel (the large-grid tiles are exercised at full scale in test_linear_gpu.py),
+ragged M/N/K, strides and offsets on every operand, alpha, the four activations and the three
+epilogues. Sizes keep the float64 oracle to a few seconds in total.
 """
 
 from __future__ import annotations
