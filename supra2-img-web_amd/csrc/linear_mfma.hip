@@ -128,30 +128,35 @@ __global__ __launch_bounds__(256, 2) void linear_mfma_kernel(LinearParams p, int
     boff[n] = 4u * (unsigned)(min(row, nlast) * (int)p.ldw + 4 * c);
   }
 
+  // Copies through buffer descriptors: the tile's first row is the descriptor base (scalar), the
+  // k-tile's column offset the scalar soffset, and the lane's row/chunk offset a loop-invariant
+  // 32-bit voffset, so the copies need no per-lane address arithmetic (VALU work serializes with
+  // the MFMAs on a SIMD).
+  const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(xbase);
+  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(wbase);
   const int nkt = (p.K + BK - 1) / BK;
   auto issue = [&](int kt) {
     float* at = lds + (kt % NS) * STAGE;
     float* bt = at + A_TILE;
     const int k0 = kt * BK;
-    const char* xa = reinterpret_cast<const char*>(xbase + k0);
-    const char* wb = reinterpret_cast<const char*>(wbase + k0);
+    const unsigned soff = 4u * (unsigned)k0;
     if (k0 + BK <= p.K) {
 #pragma unroll
-      for (int n = 0; n < NIA; ++n) load_to_lds16(xa + aoff[n], at + (n * 4 + wave) * 256);
+      for (int n = 0; n < NIA; ++n) buffer_to_lds16(xr, aoff[n], at + (n * 4 + wave) * 256, soff);
 #pragma unroll
-      for (int n = 0; n < NIB; ++n) load_to_lds16(wb + boff[n], bt + (n * 4 + wave) * 256);
+      for (int n = 0; n < NIB; ++n) buffer_to_lds16(wr, boff[n], bt + (n * 4 + wave) * 256, soff);
     } else {
       // the k-tile holding K: columns at or past K re-read the last group (never multiplied)
       const int kmax = p.K - 8 - k0;
 #pragma unroll
       for (int n = 0; n < NIA; ++n) {
         const int shift = acol[n] > kmax + 4 ? (acol[n] & ~7) - kmax : 0;  // whole groups back
-        load_to_lds16(xa + aoff[n] - 4 * shift, at + (n * 4 + wave) * 256);
+        buffer_to_lds16(xr, aoff[n] - 4u * (unsigned)shift, at + (n * 4 + wave) * 256, soff);
       }
 #pragma unroll
       for (int n = 0; n < NIB; ++n) {
         const int shift = bcol[n] > kmax + 4 ? (bcol[n] & ~7) - kmax : 0;
-        load_to_lds16(wb + boff[n] - 4 * shift, bt + (n * 4 + wave) * 256);
+        buffer_to_lds16(wr, boff[n] - 4u * (unsigned)shift, bt + (n * 4 + wave) * 256, soff);
       }
     }
   };
@@ -343,9 +348,11 @@ hipError_t launch_act(const LinearParams& p, hipStream_t stream) {
 
 bool linear_mfma_supported(const LinearParams& p) {
   auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  // copies address a tile's rows as 32-bit byte offsets from its first row (up to 128 x rows and
+  // 192 W rows, plus the k offset <= the row stride); stores address up to 128 output rows likewise
   return p.K % 8 == 0 && a16(p.x) && a16(p.w) && p.x_off % 4 == 0 && p.ldx % 4 == 0 && p.ldw % 4 == 0 &&
-         (int64_t)64 * 2 * p.ldx * 4 < 0x7fffffffLL && (int64_t)64 * 3 * p.ldw * 4 < 0x7fffffffLL &&
-         (int64_t)64 * 2 * p.ldy < 0x7fffffffLL;
+         (int64_t)(64 * 2 + 1) * p.ldx * 4 < 0x7fffffffLL && (int64_t)(64 * 3 + 1) * p.ldw * 4 < 0x7fffffffLL &&
+         (int64_t)64 * 2 * p.ldy * 4 < 0x7fffffffLL;
 }
 
 LinearTile linear_mfma_tile(const LinearParams& p, int num_cus) {
