@@ -356,20 +356,17 @@ bool linear_mfma_supported(const LinearParams& p) {
 }
 
 LinearTile linear_mfma_tile(const LinearParams& p, int num_cus) {
-  // Measured on the DiT layers at 16384 rows (after a warm-up, per layer, eight tile / k-depth /
-  // stage variants): wide outputs run best on 128 x 192 tiles (qkv N = 1728: 283 us; fc1 N = 2304:
-  // 350 us; 128 x 64 tiles: 286 and 368), the 576-wide layers on 64 x 64 tiles at five workgroups per
-  // CU (proj/q/cproj 101 us, fc2 384 us; 128 x 64: 106 and 406). 64 x 64 tiles also spread small
-  // calls (the 1024-row VAE projections, per-prompt context projections) over more CUs.
-  // Then 64 x 192 tiles (one 32 x 96 strip per wave, each x operand read feeding three MFMAs),
-  // measured per layer: qkv 283 -> 269 us (k-depth 32, 2 stages); the 576-wide layers at three
-  // workgroups per CU with k-depth 16 and 3 stages: proj/q/cproj 101 -> 99.4 us, fc2 384 -> 369 us
-  // (fc1 stays on 128 x 192: 364 us with 64 x 192).
+  // Measured per layer on the DiT linears at 16384 rows (after a warm-up; seven tile / k-depth /
+  // stage variants): 128 x 192 tiles (2 x 3 accumulators per wave, k-depth 32, two stages) for the
+  // 2304-wide fc1 (324 us; 64 x 192: 336 us); 64 x 192 tiles (one 32 x 96 strip per wave, each x
+  // operand read feeding three MFMAs) with k-depth 16 and three stages at three workgroups per CU
+  // for qkv (245 us; k-depth 32 / two stages 254, 128 x 192 271) and the 576-wide layers (proj/q/
+  // cproj 85-88 us, fc2 320 us; 64 x 64: 90-95 and 337). 64 x 64 tiles spread small calls (the
+  // 1024-row VAE projections, per-prompt context projections, batch-2 calls) over more CUs.
   const int64_t tiles_wide = ((p.M + 127) / 128) * ((p.N + 191) / 192);
   const int64_t tiles_tall = ((p.M + 63) / 64) * ((p.N + 191) / 192);
   if (p.N >= 2048 && tiles_wide >= num_cus) return {2, 3, 32, 2};
-  if (p.N >= 1024 && tiles_tall >= 4 * (int64_t)num_cus) return {1, 3, 32, 2};
-  if (p.N % 192 == 0 && tiles_tall >= 3 * (int64_t)num_cus) return {1, 3, 16, 3};
+  if ((p.N % 192 == 0 || p.N >= 1024) && tiles_tall >= 3 * (int64_t)num_cus) return {1, 3, 16, 3};
   return {1, 1, 32, 2};
 }
 
@@ -377,7 +374,7 @@ const char* linear_kernel_name(const LinearParams& p, int num_cus) {
   if (!linear_mfma_supported(p)) return "linear_generic";
   const LinearTile t = linear_mfma_tile(p, num_cus);
   if (t.wm == 2) return "linear_mfma_128x192";
-  if (t.wn == 3) return t.bk == 16 ? "linear_mfma_64x192_bk16" : "linear_mfma_64x192";
+  if (t.wn == 3) return "linear_mfma_64x192";
   return "linear_mfma_64x64";
 }
 
@@ -390,7 +387,7 @@ hipError_t launch_linear(const LinearParams& p, int num_cus, hipStream_t stream)
   }
   const LinearTile t = linear_mfma_tile(p, num_cus);
   if (t.wm == 2) return launch_act<2, 3, 32, 2>(p, stream);
-  if (t.wn == 3) return t.bk == 16 ? launch_act<1, 3, 16, 3>(p, stream) : launch_act<1, 3, 32, 2>(p, stream);
+  if (t.wn == 3) return launch_act<1, 3, 16, 3>(p, stream);
   return launch_act<1, 1, 32, 2>(p, stream);
 }
 

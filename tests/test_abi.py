@@ -273,8 +273,8 @@ def test_linear_kernel_choice():
     # DiT layers at batch 64 (16384 rows): 64 x 192 or 128 x 192 tiles while the grid fills the chip, else 64 x 64
     assert _lib.linear_kernel_name(lin_args(M=16384, N=1728, K=576)) == "linear_mfma_64x192"       # qkv
     assert _lib.linear_kernel_name(lin_args(M=16384, N=2304, K=576)) == "linear_mfma_128x192"      # fc1
-    assert _lib.linear_kernel_name(lin_args(M=16384, N=576, K=576)) == "linear_mfma_64x192_bk16"   # proj, q, cproj
-    assert _lib.linear_kernel_name(lin_args(M=16384, N=576, K=2304)) == "linear_mfma_64x192_bk16"  # fc2
+    assert _lib.linear_kernel_name(lin_args(M=16384, N=576, K=576)) == "linear_mfma_64x192"        # proj, q, cproj
+    assert _lib.linear_kernel_name(lin_args(M=16384, N=576, K=2304)) == "linear_mfma_64x192"       # fc2
     assert _lib.linear_kernel_name(lin_args(M=512, N=1728, K=576)) == "linear_mfma_64x64"          # batch 2
     assert _lib.linear_kernel_name(lin_args(M=4096, N=600, K=576)) == "linear_mfma_64x64"
     assert _lib.linear_kernel_name(lin_args(M=77, N=1152, K=576)) == "linear_mfma_64x64"  # small call: 64 x 64 tiles

@@ -82,10 +82,10 @@ def test_dit_qkv_full_batch(dev):
     run_checked(dev, call, check_fp64=False)
 
 
-@pytest.mark.parametrize("M,N,K,tile", [(16001, 1100, 584, "64x192"), (16371, 576, 2312, "64x192_bk16"),
-                                        (12345, 2113, 520, "128x192"), (16384, 576, 16, "64x192_bk16")])
+@pytest.mark.parametrize("M,N,K,tile", [(16001, 1100, 584, "64x192"), (16371, 576, 2312, "64x192"),
+                                        (12345, 2113, 520, "128x192"), (16384, 576, 16, "64x192")])
 def test_large_tiles_ragged(dev, M, N, K, tile):
-    """Each large-grid tile at full scale with ragged M, N and K (k-tiles cut at K % 32 == 8)."""
+    """Each large-grid tile at full scale with ragged M and N, and K % 16 == 8 where K is ragged."""
     call = make_linear(f"large_{M}x{N}x{K}", M, N, K, seed=M % 97 + N + K, act=_lib.SA_ACT_GELU_TANH,
                        epi=_lib.SA_EPI_RESID_GATE, gate_off=3)
     run_checked(dev, call, expect_kernel=f"linear_mfma_{tile}", check_fp64=False)
