@@ -8,11 +8,13 @@
 // Two kernels, both spread over the whole chip (one workgroup per group, as the reference runs it,
 // would use 32 of 256 CUs):
 //   1. statistics: workgroup (g, s) takes a chunk of pixels of group g and writes its count, mean
-//      and centred sum of squares (a mean pass, then a centred pass over the chunk: the reference's
-//      two-pass form, for accuracy);
-//   2. apply: each workgroup combines the chunk statistics of every group (Chan et al.'s pairwise
-//      update: exact in exact arithmetic, no E[x^2] - E[x]^2 cancellation) into LDS, then normalizes
-//      whole pixel rows.
+//      and centred sum of squares;
+//   2. apply: each of about two workgroups per CU combines the chunk statistics of every group,
+//      then normalizes its slice of the image.
+// Both read and write float4 items when the group width, C and the pointers allow it.
+
+#include <algorithm>
+#include <stdint.h>
 
 #include "common.h"
 #include "kernels.h"
@@ -20,8 +22,6 @@
 namespace sa {
 
 namespace {
-
-constexpr int kGnRows = 8;  // pixel rows per apply workgroup
 
 // Sum over the 256 threads of the workgroup: cross-lane shuffles within each wave, then the four
 // wave sums through LDS.
@@ -36,8 +36,34 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return s;
 }
 
+// One pixel's slice of its group holds cg channels: with VEC (cg, C and the pointers multiples
+// of 4 floats / 16 bytes) it is read as cg/4 float4 items, otherwise as cg floats.
+template <bool VEC>
+__device__ __forceinline__ float item_sum(const float* p) {
+  if constexpr (VEC) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(p);
+    return (v[0] + v[1]) + (v[2] + v[3]);
+  }
+  return *p;
+}
+
+template <bool VEC>
+__device__ __forceinline__ float item_sq(const float* p, float mean) {
+  if constexpr (VEC) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(p);
+    float q = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) q = fmaf(v[k] - mean, v[k] - mean, q);
+    return q;
+  }
+  const float d = *p - mean;
+  return d * d;
+}
+
 // part[(g * S + s) * 3 + {0, 1, 2}] = count, mean, centred sum of squares of pixels
-// [s * chunk, min((s + 1) * chunk, HW)) of group g.
+// [s * chunk, min((s + 1) * chunk, HW)) of group g (a mean pass, then a centred pass over the
+// chunk: the reference's two-pass form, for accuracy).
+template <bool VEC>
 __global__ __launch_bounds__(256) void groupnorm_stats_kernel(const float* __restrict__ x, float* __restrict__ part,
                                                               int HW, int C, int cg, int S, int chunk) {
   __shared__ float red[4];
@@ -45,15 +71,20 @@ __global__ __launch_bounds__(256) void groupnorm_stats_kernel(const float* __res
   const int s = blockIdx.x % S;
   const int p0 = s * chunk;
   const int np = max(0, min(chunk, HW - p0));
+  const int w = VEC ? cg / 4 : cg;  // items per pixel slice
+  const int64_t items = (int64_t)np * w;
   const int64_t n = (int64_t)np * cg;
   const float* base = x + (int64_t)p0 * C + g * cg;
   float acc = 0.f;
-  for (int64_t i = threadIdx.x; i < n; i += 256) acc += base[(i / cg) * C + i % cg];
+  for (int64_t i = threadIdx.x; i < items; i += 256) {
+    const int64_t pix = i / w;
+    acc += item_sum<VEC>(base + pix * C + (VEC ? 4 : 1) * (i - pix * w));
+  }
   const float mean = n > 0 ? block_sum(acc, red) / (float)n : 0.f;
   float m2 = 0.f;
-  for (int64_t i = threadIdx.x; i < n; i += 256) {
-    const float d = base[(i / cg) * C + i % cg] - mean;
-    m2 = fmaf(d, d, m2);
+  for (int64_t i = threadIdx.x; i < items; i += 256) {
+    const int64_t pix = i / w;
+    m2 += item_sq<VEC>(base + pix * C + (VEC ? 4 : 1) * (i - pix * w), mean);
   }
   m2 = n > 0 ? block_sum(m2, red) : 0.f;
   if (threadIdx.x == 0) {
@@ -63,35 +94,90 @@ __global__ __launch_bounds__(256) void groupnorm_stats_kernel(const float* __res
   }
 }
 
+// Each workgroup combines the chunk statistics of every group (Chan et al.'s pairwise update:
+// exact in exact arithmetic, no E[x^2] - E[x]^2 cancellation) - with STAGED the 3*G*S values are
+// first copied to LDS in one coalesced pass, so the per-group loops read LDS instead of making a
+// chain of dependent global loads - then normalizes items [i0, i0 + per_block) of the image
+// (float4 items when VEC).
+template <bool VEC, bool STAGED>
 __global__ __launch_bounds__(256) void groupnorm_apply_kernel(const float* __restrict__ x, const float* __restrict__ part,
                                                               const float* __restrict__ gamma,
                                                               const float* __restrict__ beta, float* __restrict__ y,
-                                                              int HW, int C, int cg, int G, int S, float eps) {
-  extern __shared__ float stats[];  // [G][2]: mean, rstd
+                                                              int HW, int C, int cg, int G, int S, float eps,
+                                                              int64_t per_block) {
+  extern __shared__ float sm[];  // [G][2]: mean, rstd; then (STAGED) the [G*S][3] chunk statistics
+  float* stats = sm;
+  const float* src = part;
+  if constexpr (STAGED) {
+    float* staged = sm + 2 * G;
+    for (int i = threadIdx.x; i < 3 * G * S; i += 256) staged[i] = part[i];
+    __syncthreads();
+    src = staged;
+  }
   for (int g = threadIdx.x; g < G; g += 256) {
     float n = 0.f, mean = 0.f, m2 = 0.f;
     for (int s = 0; s < S; ++s) {
-      const float nb = part[3 * (g * S + s)];
+      const float* e = src + 3 * (g * S + s);
+      const float nb = e[0];
       if (nb == 0.f) continue;
-      const float mb = part[3 * (g * S + s) + 1];
       const float n_new = n + nb;
-      const float d = mb - mean;
+      const float d = e[1] - mean;
       mean += d * (nb / n_new);
-      m2 += part[3 * (g * S + s) + 2] + d * d * (n * nb / n_new);
+      m2 += e[2] + d * d * (n * nb / n_new);
       n = n_new;
     }
     stats[2 * g] = mean;
     stats[2 * g + 1] = rsqrtf(m2 / n + eps);
   }
   __syncthreads();
-  const int p0 = blockIdx.x * kGnRows;
-  const int rows = min(kGnRows, HW - p0);
-  for (int i = threadIdx.x; i < rows * C; i += 256) {
-    const int c = i % C;
-    const int g = c / cg;
-    const int64_t e = (int64_t)p0 * C + i;
-    y[e] = fmaf((x[e] - stats[2 * g]) * stats[2 * g + 1], gamma[c], beta[c]);
+  const int w = VEC ? C / 4 : C;  // items per pixel row
+  const int64_t total = (int64_t)HW * w;
+  const int64_t i0 = (int64_t)blockIdx.x * per_block;
+  const int64_t i1 = min(total, i0 + per_block);
+  for (int64_t i = i0 + threadIdx.x; i < i1; i += 256) {
+    const int64_t row = i / w;
+    const int c = (VEC ? 4 : 1) * (int)(i - row * w);
+    const int g = c / cg;  // with VEC the four channels share a group (cg % 4 == 0)
+    const float mean = stats[2 * g], rstd = stats[2 * g + 1];
+    const int64_t e = row * C + c;
+    if constexpr (VEC) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(x + e);
+      const f32x4 ga = *reinterpret_cast<const f32x4*>(gamma + c);
+      const f32x4 be = *reinterpret_cast<const f32x4*>(beta + c);
+      f32x4 o;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) o[k] = fmaf((v[k] - mean) * rstd, ga[k], be[k]);
+      *reinterpret_cast<f32x4*>(y + e) = o;
+    } else {
+      y[e] = fmaf((x[e] - mean) * rstd, gamma[c], beta[c]);
+    }
   }
+}
+
+template <bool VEC>
+hipError_t launch_vec(const float* x, const float* gamma, const float* beta, float* y, float* part, int HW, int C,
+                      int groups, float eps, hipStream_t stream) {
+  const int S = groupnorm_chunks(HW, groups);
+  const int chunk = (HW + S - 1) / S;
+  hipLaunchKernelGGL(groupnorm_stats_kernel<VEC>, dim3(groups * S), dim3(256), 0, stream, x, part, HW, C, C / groups,
+                     S, chunk);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  // about two workgroups per CU of 256-item slices
+  const int64_t total = (int64_t)HW * (VEC ? C / 4 : C);
+  const int64_t per_block = std::max<int64_t>(256, ((total + 511) / 512 + 255) / 256 * 256);
+  const int64_t blocks = (total + per_block - 1) / per_block;
+  if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
+  const size_t staged_bytes = (size_t)(2 * groups + 3 * groups * S) * sizeof(float);
+  if (staged_bytes <= 48 * 1024) {
+    hipLaunchKernelGGL((groupnorm_apply_kernel<VEC, true>), dim3((unsigned)blocks), dim3(256), staged_bytes, stream, x,
+                       part, gamma, beta, y, HW, C, C / groups, groups, S, eps, per_block);
+  } else {
+    hipLaunchKernelGGL((groupnorm_apply_kernel<VEC, false>), dim3((unsigned)blocks), dim3(256),
+                       (size_t)groups * 2 * sizeof(float), stream, x, part, gamma, beta, y, HW, C, C / groups, groups,
+                       S, eps, per_block);
+  }
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -105,15 +191,10 @@ int groupnorm_chunks(int HW, int groups) {
 hipError_t launch_groupnorm(const float* x, const float* gamma, const float* beta, float* y, float* part, int HW, int C,
                             int groups, float eps, hipStream_t stream) {
   if (groups <= 0 || C % groups != 0 || (int64_t)groups * 2 * 4 > 64 * 1024) return hipErrorInvalidValue;
-  const int S = groupnorm_chunks(HW, groups);
-  const int chunk = (HW + S - 1) / S;
-  hipLaunchKernelGGL(groupnorm_stats_kernel, dim3(groups * S), dim3(256), 0, stream, x, part, HW, C, C / groups, S,
-                     chunk);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(groupnorm_apply_kernel, dim3((HW + kGnRows - 1) / kGnRows), dim3(256), groups * 2 * sizeof(float),
-                     stream, x, part, gamma, beta, y, HW, C, C / groups, groups, S, eps);
-  return hipGetLastError();
+  auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  const bool vec = (C / groups) % 4 == 0 && C % 4 == 0 && a16(x) && a16(y) && a16(gamma) && a16(beta);
+  return vec ? launch_vec<true>(x, gamma, beta, y, part, HW, C, groups, eps, stream)
+             : launch_vec<false>(x, gamma, beta, y, part, HW, C, groups, eps, stream);
 }
 
 }  // namespace sa

@@ -44,10 +44,11 @@ def test_vae_mid_block(dev, in_place):
     check(got.reshape(call.HW, call.C), call)
 
 
-@pytest.mark.parametrize("HW,C,groups,bias", [(1024, 512, 32, False), (256, 256, 32, True), (100, 128, 32, True),
-                                              (64, 64, 8, True), (90, 96, 32, True)])
+@pytest.mark.parametrize("HW,C,groups,bias", [(1024, 512, 32, False), (1000, 512, 32, True), (256, 256, 32, True),
+                                              (100, 128, 32, True), (64, 64, 8, True), (90, 96, 32, True)])
 def test_other_shapes(dev, HW, C, groups, bias):
-    """D = 256 (wide kernel), 128 / 64 (flash kernel), 96 (generic kernel), ragged pixel counts."""
+    """D = 256 (wide kernel), 128 / 64 (flash kernel), 96 (generic kernel), ragged pixel counts; GroupNorm
+    on float4 items (group widths 16, 8, 4, 2... multiples of 4) and on floats (width 3)."""
     call = vae_block(HW=HW, C=C, groups=groups, bias=bias, seed=HW + C)
     print(f"[vae case] HW={HW} C={C} groups={groups} bias={bias}", flush=True)
     st = StagedVae(dev, call)
