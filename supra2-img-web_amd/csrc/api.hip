@@ -265,6 +265,7 @@ int resolve_linear(const sa_linear_args* a, sa::LinearParams* p) {
   p->y = a->y;
   p->y_off = a->y_off;
   p->ldy = ldy;
+  p->resid = nullptr;
   p->M = a->M;
   p->N = a->N;
   p->K = a->K;
@@ -409,14 +410,19 @@ int64_t sa_attention_workspace_bytes(const sa_attn_args* args) {
   return c.path == Path::kWide ? c.wide.ws_floats * (int64_t)sizeof(float) : 0;
 }
 
-int sa_linear_f32(const sa_linear_args* args, void* stream) {
+// The linear layer with an optional residual source (resid: rows laid out like y, read by the
+// residual epilogues in place of y; the caller has checked that it does not overlap y).
+static int run_linear(const sa_linear_args* args, const float* resid, void* stream) {
   sa::LinearParams p;
   const int rc = resolve_linear(args, &p);
   if (rc != SA_OK) return rc;
+  p.resid = resid;
   const hipError_t e = sa::launch_linear(p, num_cus(), (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, sa::linear_kernel_name(p, num_cus()));
   return ok();
 }
+
+int sa_linear_f32(const sa_linear_args* args, void* stream) { return run_linear(args, nullptr, stream); }
 
 const char* sa_linear_kernel_name(const sa_linear_args* args) {
   sa::LinearParams p;
@@ -484,11 +490,9 @@ int sa_vae_attention_f32(const sa_vae_attn_args* a, void* stream) {
   if (e != hipSuccess) return hip_fail(e, "groupnorm");
   if ((rc = sa_linear_f32(&l1, stream)) != SA_OK) return rc;
   if ((rc = sa_attention_f32(&at, stream)) != SA_OK) return rc;
-  if (a->out != a->x) {
-    e = hipMemcpyAsync(a->out, a->x, (size_t)(HW * C * 4), hipMemcpyDeviceToDevice, st);
-    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync");
-  }
-  if ((rc = sa_linear_f32(&l2, stream)) != SA_OK) return rc;
+  // out = x + a Wo^T + bo: the residual epilogue reads x directly when out is another buffer
+  // (checked above not to overlap x)
+  if ((rc = run_linear(&l2, a->out != a->x ? a->x : nullptr, stream)) != SA_OK) return rc;
   return ok();
 }
 

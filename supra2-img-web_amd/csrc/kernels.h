@@ -83,6 +83,9 @@ struct LinearParams {
   int64_t gate_off;
   float* y;  // [M, N] rows at y + y_off + m*ldy
   int64_t y_off, ldy;
+  // residual epilogues: the added rows are read from resid (same offset and stride as y) instead
+  // of y itself when non-null, so y = r + resid needs no copy of resid into y first
+  const float* resid;
   int M, N, K;
   float alpha;
   int act, epi;

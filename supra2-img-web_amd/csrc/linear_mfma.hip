@@ -236,6 +236,8 @@ __global__ __launch_bounds__(256, 2) void linear_mfma_kernel(LinearParams p, int
   const bool full = m0 + BM <= p.M && n0 + BN <= p.N;
   const __amdgpu_buffer_rsrc_t yr =
       __builtin_amdgcn_make_buffer_rsrc(p.y + p.y_off + (int64_t)mw * p.ldy + nw, 0, 0x7fffffff, 0x00020000);
+  const float* rsrc_base = (p.resid ? p.resid : p.y) + p.y_off + (int64_t)mw * p.ldy + nw;  // residual rows
+  const __amdgpu_buffer_rsrc_t rr_ = buffer_rsrc(rsrc_base);
   const int ldy4 = 4 * (int)p.ldy;
   auto store = [&](auto check) {
     constexpr bool kCheck = decltype(check)::value;
@@ -257,7 +259,7 @@ __global__ __launch_bounds__(256, 2) void linear_mfma_kernel(LinearParams p, int
             const int rr = 8 * (r >> 2) + (r & 3);
             old[r] = 0.f;
             if (!kCheck || (n_ok && mw + 32 * i + 4 * half + rr < p.M))
-              old[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(yr, voff, rr * ldy4, 0));
+              old[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rr_, voff, rr * ldy4, 0));
           }
         }
 #pragma unroll
@@ -307,9 +309,9 @@ __global__ __launch_bounds__(256) void linear_generic_kernel(LinearParams p) {
       case LIN_ACT_SILU: v = apply_act<LIN_ACT_SILU>(v); break;
       default: break;
     }
-    float* dst = p.y + p.y_off + (int64_t)m * p.ldy + n;
-    if (p.epi == LIN_EPI_STORE) *dst = v;
-    else *dst = fmaf(p.epi == LIN_EPI_RESID_GATE ? p.gate[p.gate_off + n] : 1.f, v, *dst);
+    const int64_t e = p.y_off + (int64_t)m * p.ldy + n;
+    if (p.epi == LIN_EPI_STORE) p.y[e] = v;
+    else p.y[e] = fmaf(p.epi == LIN_EPI_RESID_GATE ? p.gate[p.gate_off + n] : 1.f, v, (p.resid ? p.resid : p.y)[e]);
   }
 }
 
