@@ -135,18 +135,24 @@ __global__ __launch_bounds__(256, 2) void linear_mfma_kernel(LinearParams p, int
   const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(xbase);
   const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(wbase);
   const int nkt = (p.K + BK - 1) / BK;
-  auto issue = [&](int kt) {
-    float* at = lds + (kt % NS) * STAGE;
+  const int nfull = p.K / BK;  // whole k-tiles; with K % BK != 0 the last tile (nfull) holds K
+  // Copies of k-tile kt into LDS stage S. The stage is a compile-time constant (the main loop
+  // advances NS tiles at a time), so every LDS address below is a constant offset.
+  auto issue = [&](int kt, auto stage) {
+    constexpr int S = decltype(stage)::value;
+    float* at = lds + S * STAGE;
     float* bt = at + A_TILE;
-    const int k0 = kt * BK;
-    const unsigned soff = 4u * (unsigned)k0;
-    if (k0 + BK <= p.K) {
+    if (kt < nfull) {
+      const unsigned soff = 4u * (unsigned)(kt * BK);
 #pragma unroll
       for (int n = 0; n < NIA; ++n) buffer_to_lds16(xr, aoff[n], at + (n * 4 + wave) * 256, soff);
 #pragma unroll
       for (int n = 0; n < NIB; ++n) buffer_to_lds16(wr, boff[n], bt + (n * 4 + wave) * 256, soff);
     } else {
-      // the k-tile holding K: columns at or past K re-read the last group (never multiplied)
+      // the tile holding K (always tile nfull, so its offsets are loop-invariant): columns at or
+      // past K re-read the last group (never multiplied)
+      const int k0 = nfull * BK;
+      const unsigned soff = 4u * (unsigned)k0;
       const int kmax = p.K - 8 - k0;
 #pragma unroll
       for (int n = 0; n < NIA; ++n) {
@@ -179,41 +185,42 @@ __global__ __launch_bounds__(256, 2) void linear_mfma_kernel(LinearParams p, int
   // Operands of one group in registers, double-buffered: group g + 1 (or group 0 of the next
   // tile) is read from LDS while the MFMAs of group g run.
   f32x4 ra[2][WM], rb[2][WN];
-  auto read_group = [&](int kt, int g, int slot) {
-    const float* at = lds + (kt % NS) * STAGE + arow0 + goff[g];
-    const float* bt = lds + (kt % NS) * STAGE + A_TILE + brow0 + goff[g];
+  auto read_group = [&](auto stage, int g, int slot) {
+    constexpr int S = decltype(stage)::value;
+    const float* at = lds + S * STAGE + arow0 + goff[g];
+    const float* bt = lds + S * STAGE + A_TILE + brow0 + goff[g];
 #pragma unroll
     for (int i = 0; i < WM; ++i) ra[slot][i] = *reinterpret_cast<const f32x4*>(at + i * 32 * BK);
 #pragma unroll
     for (int j = 0; j < WN; ++j) rb[slot][j] = *reinterpret_cast<const f32x4*>(bt + j * 32 * BK);
   };
-  // tile kt has landed for this thread (the younger tiles may still be in flight); the barrier
-  // makes it whole and guarantees every wave has read the stage the next copies overwrite
-  auto sync_tile = [&](int kt) {
+  // tile kt (in stage S) has landed for this thread (the younger tiles may still be in flight);
+  // the barrier makes it whole and guarantees every wave has read the stage the next copies
+  // overwrite: tile kt + NS - 1 goes to stage (S + NS - 1) % NS, the one tile kt - 1 used
+  auto sync_tile = [&](int kt, auto stage) {
+    constexpr int S = decltype(stage)::value;
     if (NS == 3 && kt + 1 < nkt) {
       wait_vmcnt<(NS == 3 ? NI : 0)>();
     } else {
       wait_vmcnt<0>();
     }
     __syncthreads();
-    if (kt + NS - 1 < nkt) issue(kt + NS - 1);
+    if (kt + NS - 1 < nkt) issue(kt + NS - 1, std::integral_constant<int, (S + NS - 1) % NS>{});
   };
-
-#pragma unroll
-  for (int t = 0; t < NS - 1; ++t)
-    if (t < nkt) issue(t);
-  sync_tile(0);
-  read_group(0, 0, 0);
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int ng = min(NG, (p.K - kt * BK) >> 3);  // valid groups of 8 k in this tile
+  // the MFMAs of tile kt (stage S); the operands of group g + 1, or of the next tile's group 0,
+  // are read while those of group g are multiplied
+  auto step = [&](int kt, auto stage) {
+    constexpr int S = decltype(stage)::value;
+    constexpr int S1 = (S + 1) % NS;
+    const int ng = kt < nfull ? NG : (p.K - nfull * BK) >> 3;  // valid groups of 8 k in this tile
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       const int cur = g & 1;  // NG is even, so group 0 of every tile sits in slot 0
       if (g + 1 < NG) {
-        read_group(kt, g + 1, cur ^ 1);
+        read_group(stage, g + 1, cur ^ 1);
       } else if (kt + 1 < nkt) {
-        sync_tile(kt + 1);
-        read_group(kt + 1, 0, cur ^ 1);
+        sync_tile(kt + 1, std::integral_constant<int, S1>{});
+        read_group(std::integral_constant<int, S1>{}, 0, cur ^ 1);
       }
       if (g < ng) {
 #pragma unroll
@@ -225,7 +232,23 @@ __global__ __launch_bounds__(256, 2) void linear_mfma_kernel(LinearParams p, int
               acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(ra[cur][i][s], rb[cur][j][s], acc[i][j], 0, 0, 0);
       }
     }
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1c = std::integral_constant<int, 1>;
+  using S2c = std::integral_constant<int, 2 % NS>;
+
+  issue(0, S0{});  // tile 0 (a tile always exists: K >= 8)
+  if (NS == 3 && nkt > 1) issue(1, S1c{});
+  sync_tile(0, S0{});
+  read_group(S0{}, 0, 0);
+  int kt = 0;
+  for (; kt + NS <= nkt; kt += NS) {  // tile kt + u sits in stage u
+    step(kt, S0{});
+    step(kt + 1, S1c{});
+    if constexpr (NS == 3) step(kt + 2, S2c{});
   }
+  if (kt < nkt) step(kt, S0{});
+  if (NS == 3 && kt + 1 < nkt) step(kt + 1, S1c{});
 
   // ---- epilogue: lane holds column n = nw + 32j + col, rows mw + 32i + 8(r/4) + 4*half + r%4.
   // Buffer loads/stores over the wave's output block: a scalar descriptor, a 32-bit per-lane
