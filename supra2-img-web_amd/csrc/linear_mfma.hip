@@ -16,8 +16,10 @@
 //   k = 8g + 4h + s at MFMA step s (s = 0..3): one b128 LDS read per operand row and group feeds
 //   four MFMAs, and every (x, W) pair of k meets exactly once.
 //
-// Tiles move HBM/L2 -> LDS with global_load_lds_dwordx4 (no VGPR staging), NS stages, one barrier
-// per k-tile. LDS rows are BK floats (BK/4 chunks of 16 bytes); chunk c of row r sits at
+// Tiles move HBM/L2 -> LDS with buffer_load_dwordx4 ... lds (no VGPR staging; scalar descriptor and
+// k offset, loop-invariant lane offsets), NS stages, one barrier per k-tile. The k-loop advances NS
+// tiles at a time so every stage index is a compile-time constant: the steady-state loop issues
+// no VALU instruction, which on gfx950 would serialize with the MFMAs of the SIMD. LDS rows are BK floats (BK/4 chunks of 16 bytes); chunk c of row r sits at
 // c ^ ((r / RP) % (BK/4)) with RP = 64/BK rows per 256 bytes, which makes the b128 operand reads of
 // 16 consecutive rows conflict-free (measured SQ_LDS_BANK_CONFLICT = 0). The operands of the next
 // group of 8 k are read from LDS while the MFMAs of the current group run, and the barrier of the
