@@ -20,8 +20,9 @@
 // k offset, loop-invariant lane offsets), NS stages, one barrier per k-tile. The k-loop advances NS
 // tiles at a time so every stage index is a compile-time constant: the steady-state loop issues
 // no VALU instruction, which on gfx950 would serialize with the MFMAs of the SIMD. LDS rows are
-// BK floats (BK/4 chunks of 16 bytes); chunk c of row r sits at c ^ ((r / RP) % (BK/4)) with RP = 64/BK rows per 256 bytes, which makes the b128 operand reads of
-// 16 consecutive rows conflict-free (measured SQ_LDS_BANK_CONFLICT = 0). The operands of the next
+// BK floats (BK/4 chunks of 16 bytes); chunk c of row r sits at c ^ ((r / RP) % (BK/4)) with
+// RP = 64/BK rows per 256 bytes, which makes the b128 operand reads of 16 consecutive rows
+// conflict-free (measured SQ_LDS_BANK_CONFLICT = 0). The operands of the next
 // group of 8 k are read from LDS while the MFMAs of the current group run, and the barrier of the
 // next k-tile sits before the last group's MFMAs.
 //
