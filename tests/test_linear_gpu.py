@@ -83,9 +83,12 @@ def test_dit_qkv_full_batch(dev):
 
 
 @pytest.mark.parametrize("M,N,K,tile", [(16001, 1100, 584, "64x192"), (16371, 576, 2312, "64x192"),
-                                        (12345, 2113, 520, "128x192"), (16384, 576, 16, "64x192")])
+                                        (12345, 2113, 520, "128x192"), (16384, 576, 16, "64x192"),
+                                        (16384, 576, 560, "64x192"), (16330, 576, 552, "64x192")])
 def test_large_tiles_ragged(dev, M, N, K, tile):
-    """Each large-grid tile at full scale with ragged M and N, and K % 16 == 8 where K is ragged."""
+    """Each large-grid tile at full scale with ragged M and N, and K % 16 == 8 where K is ragged. The k-loop
+    runs its stages in groups of NS tiles: these K leave 0, 1 or 2 tiles after the last group (the 64 x 192 tile
+    has NS = 3, k-depth 16: K = 576 / 584 / 560 give 36 / 37 / 35 tiles), with and without a partial last tile."""
     call = make_linear(f"large_{M}x{N}x{K}", M, N, K, seed=M % 97 + N + K, act=_lib.SA_ACT_GELU_TANH,
                        epi=_lib.SA_EPI_RESID_GATE, gate_off=3)
     run_checked(dev, call, expect_kernel=f"linear_mfma_{tile}", check_fp64=False)
