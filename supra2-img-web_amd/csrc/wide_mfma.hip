@@ -283,31 +283,36 @@ __global__ __launch_bounds__(256) void wide_merge_kernel(AttnParams p, int q_gro
   const int qi = g * 32 + qq;
   if (qi >= p.Lq) return;
   const float* recs = ws + r * nks * REC;
-  // Chunks go in groups of 4 whose loads are all issued before any is used (indexes clamped to
-  // the last chunk, surplus lanes of a group masked out), so a query costs ceil(nks/4) load round
-  // trips per pass instead of nks.
+  // One pass over the chunks in groups of 8 whose loads are all issued before any is used
+  // (indexes clamped to the last chunk, surplus entries of a group skipped), with a running
+  // maximum: the sums so far are rescaled when a group raises it. A query costs ceil(nks/8) load
+  // round trips (one for the VAE call's 8 chunks); with a single group the rescale only touches
+  // the zero-initialized sums, so the result equals the two-pass (maximum first) merge bit for bit.
   float mt = kMaxSeed;
-  for (int c0 = 0; c0 < nks; c0 += 4) {
-    float mv[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) mv[u] = recs[(int64_t)min(c0 + u, nks - 1) * REC + 32 * D + qq];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) mt = fmaxf(mt, mv[u]);  // a repeated last chunk changes nothing
-  }
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   float lsum = 0.f;
-  for (int c0 = 0; c0 < nks; c0 += 4) {
-    float mv[4], lv[4];
-    f32x4 xv[4];
+  for (int c0 = 0; c0 < nks; c0 += 8) {
+    float mv[8], lv[8];
+    f32x4 xv[8];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < 8; ++u) {
       const float* rc = recs + (int64_t)min(c0 + u, nks - 1) * REC;
       mv[u] = rc[32 * D + qq];
       lv[u] = rc[32 * D + 32 + qq];
       xv[u] = *reinterpret_cast<const f32x4*>(rc + qq * D + 4 * d4);
     }
+    float mg = mt;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < 8; ++u) mg = fmaxf(mg, mv[u]);  // a repeated last chunk changes nothing
+    const float sc = fast_exp2(mt - mg);
+    lsum *= sc;
+    acc[0] *= sc;
+    acc[1] *= sc;
+    acc[2] *= sc;
+    acc[3] *= sc;
+    mt = mg;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
       if (c0 + u >= nks) break;
       const float a = fast_exp2(mv[u] - mt);
       lsum = fmaf(lv[u], a, lsum);
