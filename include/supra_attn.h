@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SA_ABI_VERSION 3
+#define SA_ABI_VERSION 4
 
 /* ---- status codes ---- */
 #define SA_OK 0
@@ -125,8 +125,44 @@ int sa_attention_f32(const sa_attn_args* args, void* stream);
 int64_t sa_attention_workspace_bytes(const sa_attn_args* args);
 
 /* Which kernel sa_attention_f32 would launch for these arguments (a static name such as
- * "flash_mfma_d64"), or NULL with sa_last_error() set if the arguments are rejected. Host only. */
+ * "flash_mfma_d64"), or NULL with sa_last_error() set if the arguments are rejected (the status
+ * is then sa_last_status()). Host only. */
 const char* sa_attention_kernel_name(const sa_attn_args* args);
+
+/* ---- kernel plan: the compiled kernel a call launches, and every compiled variant ----
+ * The reference picks a matmul tile (app/gpu/ops.js:15-31) and decides fused vs unfused
+ * (ops.js:111-112) inside the operator; these host-only queries make the equivalent choice of
+ * this library inspectable, so tests can show that every compiled variant runs. */
+#define SA_KERNEL_FLASH 1   /* flash_mfma_kernel<head_dim, key_split, bias_mode, mask_variant> */
+#define SA_KERNEL_WIDE 2    /* wide_mfma_kernel<head_dim, mask_variant>, + a merge kernel when key_chunks > 1 */
+#define SA_KERNEL_GENERIC 3 /* generic_kernel (any head dim <= 1024, any alignment) */
+/* mask_variant beyond the SA_MASK_* values: per-sequence key lengths plus the longest-first
+ * sequence schedule (SA_MASK_KEY_LEN with key_len_host, 8 <= B <= 256, order not the identity) */
+#define SA_MASK_VARIANT_KEY_LEN_SCHEDULED 3
+
+typedef struct sa_attn_plan {
+  uint32_t struct_size;    /* set to sizeof(sa_attn_plan) before the call */
+  int32_t kernel;          /* SA_KERNEL_* */
+  int32_t head_dim;        /* head dim the kernel is compiled for (the call's D for GENERIC) */
+  int32_t key_split;       /* FLASH: waves of a workgroup that split one query group's key blocks */
+  int32_t key_chunks;      /* WIDE: workgroups that split one query group's keys (merged after) */
+  int32_t bias_mode;       /* SA_BIAS_* compiled into the kernel */
+  int32_t mask_variant;    /* SA_MASK_* compiled into the kernel, or SA_MASK_VARIANT_KEY_LEN_SCHEDULED */
+  int32_t keys_per_step;   /* FLASH: keys a workgroup stages per loop step (32 per splitting wave); WIDE: keys per chunk */
+  int64_t workgroups;      /* grid of the attention kernel */
+  int64_t workspace_bytes; /* sa_attention_workspace_bytes(args) */
+  const char* name;        /* sa_attention_kernel_name(args) (static storage) */
+} sa_attn_plan;
+
+/* Fills *plan for these arguments: SA_OK, or the status sa_attention_f32 would return for a
+ * rejected call (nothing is launched either way). Host only. */
+int sa_attention_plan(const sa_attn_args* args, sa_attn_plan* plan);
+
+/* Number of compiled kernel variants; sa_attention_variant(i, plan) describes variant i
+ * (kernel, head_dim, key_split, bias_mode, mask_variant, name; the other fields 0). FLASH
+ * variants come first, one per <head_dim, key_split, bias_mode, mask_variant>. Host only. */
+int32_t sa_attention_variant_count(void);
+int sa_attention_variant(int32_t index, sa_attn_plan* plan);
 
 /* T5 bidirectional/unidirectional relative-position bucket of each relative position
  * rel = j - i for j in [0, Lk), i in [0, Lq): out[rel + Lq - 1] for the Lq + Lk - 1 values of rel.
@@ -165,6 +201,10 @@ int sa_event_elapsed_ms(float* ms, void* start, void* stop); /* waits for stop *
 /* ---- diagnostics ---- */
 int sa_version(void);             /* SA_ABI_VERSION */
 const char* sa_last_error(void);  /* thread-local; "" when the last call succeeded */
+/* Thread-local status of the last library call that returned one (SA_OK after a success), also
+ * for the calls whose failure is a NULL name (sa_attention_kernel_name, sa_linear_kernel_name);
+ * the reference's async errors surface the same way at sync (app/gpu/device.js:262-268). */
+int sa_last_status(void);
 
 #ifdef __cplusplus
 }

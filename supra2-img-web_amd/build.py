@@ -59,10 +59,20 @@ def _run(cmd: list[str]) -> None:
 
 
 def build_lib() -> str:
+    """Compiles each source to an object in parallel (one hipcc process per file), then links."""
+    from concurrent.futures import ThreadPoolExecutor
+
     os.makedirs(LIBDIR, exist_ok=True)
+    objdir = os.path.join(LIBDIR, "obj")
+    os.makedirs(objdir, exist_ok=True)
+    objs = [os.path.join(objdir, os.path.splitext(s)[0] + ".o") for s in HIP_SOURCES]
+    jobs = max(1, min(len(HIP_SOURCES), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4))))
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        for f in [ex.submit(_run, [_hipcc(), *HIP_FLAGS, "-c", f"-I{INCLUDE}", os.path.join(CSRC, s), "-o", o])
+                  for s, o in zip(HIP_SOURCES, objs)]:
+            f.result()
     tmp = LIB + ".tmp"
-    srcs = [os.path.join(CSRC, s) for s in HIP_SOURCES]
-    _run([_hipcc(), *HIP_FLAGS, "-shared", f"-I{INCLUDE}", *srcs, "-o", tmp])
+    _run([_hipcc(), f"--offload-arch={ARCH}", "-fPIC", "-shared", *objs, "-o", tmp])
     os.replace(tmp, LIB)
     return LIB
 

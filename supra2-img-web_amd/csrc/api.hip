@@ -26,6 +26,7 @@
 
 namespace {
 thread_local char g_err[sa::kErrorBytes] = "";
+thread_local int g_status = SA_OK;
 }  // namespace
 
 namespace sa {
@@ -35,11 +36,13 @@ int fail(int code, const char* fmt, ...) {
   va_start(ap, fmt);
   vsnprintf(g_err, sizeof(g_err), fmt, ap);
   va_end(ap);
+  g_status = code;
   return code;
 }
 
 int ok() {
   g_err[0] = '\0';
+  g_status = SA_OK;
   return SA_OK;
 }
 
@@ -147,17 +150,34 @@ int resolve(const sa_attn_args* a, sa::AttnParams* p) {
   if (overlaps(eo, eq) || overlaps(eo, ek) || overlaps(eo, ev))
     return fail(SA_ERR_ALIAS, "the output overlaps q, k or v");
 
+  // The other operands the kernels read (bias, bucket LUT, key lengths, key mask) must not overlap
+  // the output either: other workgroups write o while they are read.
+  auto span = [](const void* base, int64_t off_bytes, int64_t bytes) -> Extent {
+    uintptr_t lo = 0, hi = 0;
+    const bool ok = off_bytes >= 0 && bytes >= 0 && !__builtin_add_overflow((uintptr_t)base, (uintptr_t)off_bytes, &lo) &&
+                    !__builtin_add_overflow(lo, (uintptr_t)bytes, &hi);
+    return {lo, hi, ok};
+  };
   switch (a->bias_mode) {
     case SA_BIAS_NONE:
       break;
-    case SA_BIAS_DENSE:
+    case SA_BIAS_DENSE: {
       if (!a->bias) return fail(SA_ERR_INVALID, "SA_BIAS_DENSE needs bias");
       if (a->B > 1 && a->sbias < 0) return fail(SA_ERR_INVALID, "sbias must be >= 0");
+      const Extent eb = extent(a->bias, 0, a->sbias, 0, a->B, 1, (int64_t)a->H * a->Lq * a->Lk);
+      if (!eb.ok) return fail(SA_ERR_INVALID, "the extent of the dense bias overflows 64-bit addresses");
+      if (overlaps(eo, eb)) return fail(SA_ERR_ALIAS, "the output overlaps the dense bias");
       break;
-    case SA_BIAS_RELPOS:
+    }
+    case SA_BIAS_RELPOS: {
       if (!a->bias || !a->bucket_lut) return fail(SA_ERR_INVALID, "SA_BIAS_RELPOS needs bias (table) and bucket_lut");
       if (a->num_buckets < 1) return fail(SA_ERR_INVALID, "SA_BIAS_RELPOS needs num_buckets >= 1");
+      const Extent et = span(a->bias, 0, (int64_t)a->num_buckets * a->H * 4);
+      const Extent el = span(a->bucket_lut, 0, ((int64_t)a->Lq + a->Lk - 1) * 4);
+      if (overlaps(eo, et) || overlaps(eo, el))
+        return fail(SA_ERR_ALIAS, "the output overlaps the relative-position table or bucket LUT");
       break;
+    }
     default:
       return fail(SA_ERR_INVALID, "unknown bias_mode %d", a->bias_mode);
   }
@@ -166,12 +186,18 @@ int resolve(const sa_attn_args* a, sa::AttnParams* p) {
       break;
     case SA_MASK_KEY_LEN:
       if (!a->key_len) return fail(SA_ERR_INVALID, "SA_MASK_KEY_LEN needs key_len");
+      if (overlaps(eo, span(a->key_len, 0, (int64_t)a->B * 4)))
+        return fail(SA_ERR_ALIAS, "the output overlaps key_len");
       break;
-    case SA_MASK_KEY_MASK:
+    case SA_MASK_KEY_MASK: {
       if (!a->key_mask) return fail(SA_ERR_INVALID, "SA_MASK_KEY_MASK needs key_mask");
       if (a->B > 1 && a->smask > 0 && a->smask < a->Lk)
         return fail(SA_ERR_INVALID, "smask %lld is smaller than Lk", (long long)a->smask);
+      const int64_t sm = a->smask > 0 ? a->smask : a->Lk;
+      if (overlaps(eo, span(a->key_mask, 0, (int64_t)(a->B - 1) * sm + a->Lk)))
+        return fail(SA_ERR_ALIAS, "the output overlaps key_mask");
       break;
+    }
     default:
       return fail(SA_ERR_INVALID, "unknown mask_mode %d", a->mask_mode);
   }
@@ -514,6 +540,84 @@ const char* sa_attention_kernel_name(const sa_attn_args* args) {
   return c.name;
 }
 
+int sa_attention_plan(const sa_attn_args* args, sa_attn_plan* plan) {
+  if (plan == nullptr) return fail(SA_ERR_INVALID, "plan is NULL");
+  if (plan->struct_size != sizeof(sa_attn_plan))
+    return fail(SA_ERR_INVALID, "plan struct_size %u does not match sizeof(sa_attn_plan) = %zu", plan->struct_size,
+                sizeof(sa_attn_plan));
+  sa::AttnParams p;
+  int rc = resolve(args, &p);
+  if (rc != SA_OK) return rc;
+  Choice c;
+  rc = choose(p, &c);
+  if (rc != SA_OK) return rc;
+  *plan = sa_attn_plan{};
+  plan->struct_size = sizeof(sa_attn_plan);
+  plan->name = c.name;
+  plan->bias_mode = p.bias_mode;
+  plan->mask_variant = p.mask_mode;
+  if (c.path == Path::kFlash) {
+    const sa::FlashVariant fv = sa::flash_mfma_variant(p, c.nsplit);
+    plan->kernel = SA_KERNEL_FLASH;
+    plan->head_dim = fv.D;
+    plan->key_split = fv.nsplit;
+    plan->mask_variant = fv.mask;
+    plan->keys_per_step = 32 * fv.nsplit;
+    plan->workgroups = sa::flash_mfma_workgroups(p, c.nsplit);
+  } else if (c.path == Path::kWide) {
+    plan->kernel = SA_KERNEL_WIDE;
+    plan->head_dim = p.D;
+    plan->key_chunks = c.wide.nks;
+    plan->keys_per_step = c.wide.chunk;
+    plan->workgroups = (int64_t)p.B * p.H * c.wide.q_groups * c.wide.nks;
+    plan->workspace_bytes = c.wide.ws_floats * (int64_t)sizeof(float);
+  } else {
+    plan->kernel = SA_KERNEL_GENERIC;
+    plan->head_dim = p.D;
+    plan->workgroups = (int64_t)p.B * p.H * p.Lq;
+  }
+  return ok();
+}
+
+int32_t sa_attention_variant_count(void) {
+  // flash variants, then the wide kernel (D 256, 512 x no mask / key lengths), then generic
+  return sa::flash_mfma_variants(nullptr, 0) + 4 + 1;
+}
+
+int sa_attention_variant(int32_t index, sa_attn_plan* plan) {
+  if (plan == nullptr) return fail(SA_ERR_INVALID, "plan is NULL");
+  if (plan->struct_size != sizeof(sa_attn_plan))
+    return fail(SA_ERR_INVALID, "plan struct_size %u does not match sizeof(sa_attn_plan) = %zu", plan->struct_size,
+                sizeof(sa_attn_plan));
+  const int nflash = sa::flash_mfma_variants(nullptr, 0);
+  if (index < 0 || index >= sa_attention_variant_count())
+    return fail(SA_ERR_INVALID, "variant index %d outside [0, %d)", index, sa_attention_variant_count());
+  *plan = sa_attn_plan{};
+  plan->struct_size = sizeof(sa_attn_plan);
+  if (index < nflash) {
+    sa::FlashVariant v[128];
+    static_assert(sizeof(v) / sizeof(v[0]) >= 60, "variant table");
+    const int n = sa::flash_mfma_variants(v, 128);
+    if (n > 128) return fail(SA_ERR_UNSUPPORTED, "variant table overflow");
+    plan->kernel = SA_KERNEL_FLASH;
+    plan->head_dim = v[index].D;
+    plan->key_split = v[index].nsplit;
+    plan->bias_mode = v[index].bias;
+    plan->mask_variant = v[index].mask;
+    plan->name = sa::flash_mfma_name(v[index].D, v[index].nsplit);
+  } else if (index < nflash + 4) {
+    const int w = index - nflash;
+    plan->kernel = SA_KERNEL_WIDE;
+    plan->head_dim = w < 2 ? 256 : 512;
+    plan->mask_variant = (w & 1) ? SA_MASK_KEY_LEN : SA_MASK_NONE;
+    plan->name = sa::wide_mfma_name(plan->head_dim);
+  } else {
+    plan->kernel = SA_KERNEL_GENERIC;
+    plan->name = "generic";
+  }
+  return ok();
+}
+
 int sa_t5_bucket_lut(int32_t Lq, int32_t Lk, int32_t num_buckets, int32_t max_distance, int32_t bidirectional,
                      int32_t* out) {
   if (Lq < 1 || Lk < 1 || !out) return fail(SA_ERR_INVALID, "Lq, Lk must be >= 1 and out non-NULL");
@@ -689,6 +793,8 @@ int sa_event_elapsed_ms(float* ms, void* start, void* stop) {
 int sa_version(void) { return SA_ABI_VERSION; }
 
 const char* sa_last_error(void) { return g_err; }
+
+int sa_last_status(void) { return g_status; }
 
 }  // extern "C"
 

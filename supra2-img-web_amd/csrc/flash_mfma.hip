@@ -492,6 +492,41 @@ const char* flash_mfma_name(int D, int nsplit) {
   return nullptr;
 }
 
+// The key splits compiled per head dim: launch_flash_mfma instantiates every (bias, mask) pair for
+// each of them.
+constexpr int kSplits64[] = {1, 2, 4};
+constexpr int kSplits128[] = {1, 2};
+
+static int compiled_split(int D, int nsplit) {
+  if (D == 64) return nsplit >= 4 ? 4 : nsplit == 2 ? 2 : 1;
+  return nsplit >= 2 ? 2 : 1;
+}
+
+FlashVariant flash_mfma_variant(const AttnParams& p, int nsplit) {
+  int mask = p.mask_mode;
+  if (mask == MASK_KEY_LEN && p.order_n > 0) mask = MASK_KEY_LEN_ORDERED;
+  return {p.D, compiled_split(p.D, nsplit), p.bias_mode, mask};
+}
+
+int64_t flash_mfma_workgroups(const AttnParams& p, int nsplit) {
+  const int qt = 32 * (4 / compiled_split(p.D, nsplit));
+  return (int64_t)p.B * p.H * ((p.Lq + qt - 1) / qt);
+}
+
+int flash_mfma_variants(FlashVariant* out, int cap) {
+  int n = 0;
+  auto add = [&](int D, int s) {
+    for (int bias = BIAS_NONE; bias <= BIAS_RELPOS; ++bias)
+      for (int mask = MASK_NONE; mask <= MASK_KEY_LEN_ORDERED; ++mask) {
+        if (n < cap) out[n] = {D, s, bias, mask};
+        ++n;
+      }
+  };
+  for (int s : kSplits64) add(64, s);
+  for (int s : kSplits128) add(128, s);
+  return n;
+}
+
 hipError_t launch_flash_mfma(const AttnParams& p, int nsplit, int num_cus, hipStream_t stream) {
   if (p.D == 64) {
     if (nsplit == 4) return launch_split<64, 4>(p, num_cus, stream);

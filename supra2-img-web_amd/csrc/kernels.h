@@ -47,6 +47,18 @@ constexpr int MASK_KEY_LEN_ORDERED = 3;
 hipError_t launch_flash_mfma(const AttnParams& p, int nsplit, int num_cus, hipStream_t stream);
 const char* flash_mfma_name(int D, int nsplit);
 
+// One compiled flash_mfma_kernel instantiation: <D, nsplit, bias (BIAS_*), mask (MASK_* or
+// MASK_KEY_LEN_ORDERED)>.
+struct FlashVariant {
+  int D, nsplit, bias, mask;
+};
+// The variant a call launches with this key split.
+FlashVariant flash_mfma_variant(const AttnParams& p, int nsplit);
+// Workgroups of that launch.
+int64_t flash_mfma_workgroups(const AttnParams& p, int nsplit);
+// Every compiled variant, in a fixed order: returns the count and fills out[0, min(count, cap)).
+int flash_mfma_variants(FlashVariant* out, int cap);
+
 // Wide heads (D = 256 or 512, no bias, optional key lengths): head dim split across the waves of
 // a workgroup, keys split across workgroups, partials merged by a second kernel via a workspace.
 constexpr int kWideMaxChunks = 16;

@@ -448,7 +448,7 @@ static napi_value js_linear(napi_env env, napi_callback_info info) {
   if (fill_linear(env, argv[0], &a, &hs)) return NULL;
   /* validate before touching the device, so a bad call reports its own error on any host */
   if (sa_linear_kernel_name(&a) == NULL) {
-    throw_if(env, SA_ERR_INVALID);
+    throw_if(env, sa_last_status());
     return NULL;
   }
   if (check_linear(env, &a, &hs) || ensure_stream(env)) return NULL;
@@ -464,7 +464,7 @@ static napi_value js_linear_kernel_name(napi_env env, napi_callback_info info) {
   if (fill_linear(env, argv[0], &a, &hs)) return NULL;
   const char* name = sa_linear_kernel_name(&a);
   if (!name) {
-    throw_if(env, SA_ERR_INVALID);
+    throw_if(env, sa_last_status());
     return NULL;
   }
   napi_value r;
@@ -563,7 +563,7 @@ static napi_value js_attention(napi_env env, napi_callback_info info) {
   if (fill_args(env, argv[0], &a, &hs)) return NULL;
   /* validate before touching the device, so a bad call reports its own error on any host */
   if (sa_attention_kernel_name(&a) == NULL) {
-    throw_if(env, SA_ERR_INVALID);
+    throw_if(env, sa_last_status());
     return NULL;
   }
   if (check_attn(env, &a, &hs) || ensure_stream(env)) return NULL;
@@ -596,7 +596,7 @@ static napi_value js_kernel_name(napi_env env, napi_callback_info info) {
   if (fill_args(env, argv[0], &a, &hs)) return NULL;
   const char* name = sa_attention_kernel_name(&a);
   if (!name) {
-    throw_if(env, SA_ERR_INVALID);
+    throw_if(env, sa_last_status());
     return NULL;
   }
   napi_value r;

@@ -8,6 +8,12 @@
 // - GPU.empty / fromArray / upload / read / sync (app/gpu/device.js:144-191, 255-259).
 // - Errors: a failed call throws synchronously, with err.code set to the C ABI status
 //   ("SA_ERR_INVALID", "SA_ERR_UNSUPPORTED", "SA_ERR_HIP", "SA_ERR_ALIAS").
+// - Device lost (app/gpu/device.js:134, 208): the first SA_ERR_HIP (the HIP runtime failed: a fault,
+//   a reset, a lost device) is latched in gpu.lost, and every later operator call, read or sync
+//   throws it again instead of issuing more work.
+// - Profiler (app/gpu/device.js:272-325): GPU.create({ profile: true }) times every operator call
+//   with a HIP event pair on the device stream; gpu.profiler.report() aggregates ms and flops by
+//   operator name.
 //
 // Written for Node >= 12 (CommonJS, no optional chaining / nullish coalescing).
 "use strict";
@@ -95,14 +101,110 @@ Tensor.prototype.release = function () {
   this.buf = null;
 };
 
+// Per-operator timings aggregated by name (app/gpu/device.js:272-325). begin/end record a HIP event
+// pair on the device stream around one operator's launches; collect() waits for the recorded pairs
+// and folds them into { name, count, ms, flops } entries. Events are recycled.
+function Profiler(native, capacity) {
+  this.native = native;
+  this.capacity = capacity || 2048;
+  this.spare = [];
+  this.pending = [];
+  this.stats = new Map();
+}
+
+Profiler.prototype.event = function () {
+  return this.spare.length ? this.spare.pop() : this.native.eventCreate();
+};
+
+Profiler.prototype.begin = function (meta) {
+  var start = this.event();
+  try {
+    this.native.eventRecord(start);
+  } catch (e) {
+    this.spare.push(start);
+    throw e;
+  }
+  return { meta: meta || { name: "?", flops: 0 }, start: start, stop: null };
+};
+
+Profiler.prototype.end = function (tok) {
+  tok.stop = this.event();
+  this.native.eventRecord(tok.stop);
+  this.pending.push(tok);
+  if (this.pending.length >= this.capacity) this.collect();
+};
+
+// An operator that threw launched nothing: its start event goes back unused.
+Profiler.prototype.cancel = function (tok) {
+  this.spare.push(tok.start);
+};
+
+Profiler.prototype.collect = function () {
+  var pending = this.pending;
+  this.pending = [];
+  for (var i = 0; i < pending.length; i++) {
+    var tok = pending[i];
+    var ms = this.native.eventElapsed(tok.start, tok.stop); // waits for the stop event
+    var name = tok.meta.name || "?";
+    var s = this.stats.get(name) || { name: name, count: 0, ms: 0, flops: 0 };
+    s.count++;
+    s.ms += ms;
+    s.flops += tok.meta.flops || 0;
+    this.stats.set(name, s);
+    this.spare.push(tok.start, tok.stop);
+  }
+};
+
+Profiler.prototype.reset = function () {
+  this.stats.clear();
+};
+
+// -> Promise<[{ name, count, ms, flops }]>, most time first.
+Profiler.prototype.report = function () {
+  try {
+    this.collect();
+  } catch (e) {
+    return Promise.reject(e);
+  }
+  var rows = [];
+  this.stats.forEach(function (s) {
+    rows.push({ name: s.name, count: s.count, ms: s.ms, flops: s.flops });
+  });
+  rows.sort(function (a, b) {
+    return b.ms - a.ms;
+  });
+  return Promise.resolve(rows);
+};
+
+Profiler.prototype.destroy = function () {
+  var self = this;
+  this.pending.forEach(function (tok) {
+    self.spare.push(tok.start, tok.stop);
+  });
+  this.pending = [];
+  this.spare.forEach(function (ev) {
+    self.native.eventDestroy(ev);
+  });
+  this.spare = [];
+};
+
+function lostError(cause) {
+  var e = new Error("HIP device lost: " + (cause && cause.message ? cause.message : String(cause)));
+  e.code = "SA_ERR_HIP";
+  e.cause = cause;
+  return e;
+}
+
 function GPU(native) {
   this.native = native;
   this.pool = new BufferPool(native);
-  this.lost = false;
+  this.lost = null;
+  this.profiler = null;
 }
 
-// GPU.create({ native }) -> Promise<GPU>. Throws a named error (NoDevice) when no HIP device is
-// visible, as app/gpu/device.js:92-113 does for a missing adapter or device.
+// GPU.create({ native, profile }) -> Promise<GPU>. Throws a named error (NoDevice) when no HIP
+// device is visible, as app/gpu/device.js:92-113 does for a missing adapter or device. With
+// profile: true every operator call is timed (gpu.profiler).
 GPU.create = function (opts) {
   var native = (opts && opts.native) || loadNative();
   return new Promise(function (resolve, reject) {
@@ -112,11 +214,49 @@ GPU.create = function (opts) {
       reject(e);
       return;
     }
-    resolve(new GPU(native));
+    var gpu = new GPU(native);
+    if (opts && opts.profile) gpu.profiler = new Profiler(native);
+    resolve(gpu);
+  });
+};
+
+// Throws the latched error once the device is lost.
+GPU.prototype.check = function () {
+  if (this.lost) throw lostError(this.lost);
+};
+
+// Runs fn(), a call into the device runtime: refused once the device is lost, latches the device
+// as lost when it fails with SA_ERR_HIP.
+GPU.prototype.guard = function (fn) {
+  this.check();
+  try {
+    return fn();
+  } catch (e) {
+    if (e && e.code === "SA_ERR_HIP") this.lost = e;
+    throw e;
+  }
+};
+
+// One operator call: guard(fn), timed under meta = { name, flops } while profiling.
+GPU.prototype.op = function (meta, fn) {
+  var prof = this.profiler;
+  if (!prof) return this.guard(fn);
+  return this.guard(function () {
+    var tok = prof.begin(meta);
+    var r;
+    try {
+      r = fn();
+    } catch (e) {
+      prof.cancel(tok);
+      throw e;
+    }
+    prof.end(tok);
+    return r;
   });
 };
 
 GPU.prototype.empty = function (shape, dtype) {
+  this.check();
   var dt = dtype || "f32";
   var bytes = product(shape) * ELEMENT_BYTES[dt];
   var got = this.pool.get(bytes);
@@ -125,29 +265,52 @@ GPU.prototype.empty = function (shape, dtype) {
 
 GPU.prototype.fromArray = function (arr, shape) {
   var dt = dtypeOf(arr);
-  var t = this.empty(shape || [arr.length], dt);
-  if (product(t.shape) !== arr.length) throw new RangeError("shape does not match the array length");
-  this.native.upload(t.buf, arr, 0);
+  var sh = shape || [arr.length];
+  if (product(sh) !== arr.length) throw new RangeError("shape does not match the array length");
+  var t = this.empty(sh, dt);
+  var native = this.native;
+  try {
+    this.guard(function () {
+      native.upload(t.buf, arr, 0);
+    });
+  } catch (e) {
+    t.release();
+    throw e;
+  }
   return t;
 };
 
 GPU.prototype.write = function (t, arr, byteOffset) {
-  this.native.upload(t.buf, arr, byteOffset || 0);
+  var native = this.native;
+  this.guard(function () {
+    native.upload(t.buf, arr, byteOffset || 0);
+  });
 };
 
 // Persistent (non-pooled) buffer holding `arr`.
 GPU.prototype.upload = function (arr) {
-  var buf = this.native.malloc(Math.max(16, arr.byteLength));
-  this.native.upload(buf, arr, 0);
-  return buf;
+  var native = this.native;
+  return this.guard(function () {
+    var buf = native.malloc(Math.max(16, arr.byteLength));
+    try {
+      native.upload(buf, arr, 0);
+    } catch (e) {
+      native.free(buf);
+      throw e;
+    }
+    return buf;
+  });
 };
 
 // -> Promise<Float32Array> of the first `count` elements (all by default).
 GPU.prototype.read = function (t, count) {
   var n = count === undefined ? t.size : count;
   var out = t.dtype === "i32" ? new Int32Array(n) : t.dtype === "u8" ? new Uint8Array(n) : new Float32Array(n);
+  var native = this.native;
   try {
-    this.native.download(t.buf, out, 0);
+    this.guard(function () {
+      native.download(t.buf, out, 0);
+    });
   } catch (e) {
     return Promise.reject(e);
   }
@@ -156,13 +319,18 @@ GPU.prototype.read = function (t, count) {
 
 GPU.prototype.flush = function () {};
 
+// Waits for the stream; an asynchronous device error surfaces here (app/gpu/device.js:262-268).
 GPU.prototype.sync = function () {
+  var native = this.native;
   try {
-    this.native.sync();
+    this.guard(function () {
+      native.sync();
+    });
   } catch (e) {
     return Promise.reject(e);
   }
   return Promise.resolve();
 };
 
-module.exports = { GPU: GPU, Tensor: Tensor, BufferPool: BufferPool, loadNative: loadNative, ADDON_PATH: ADDON_PATH };
+module.exports = { GPU: GPU, Tensor: Tensor, BufferPool: BufferPool, Profiler: Profiler, loadNative: loadNative,
+                   ADDON_PATH: ADDON_PATH };

@@ -58,7 +58,9 @@ function packContexts(gpu, kvs, lens, opts) {
       e.code = "SA_ERR_INVALID";
       throw e;
     }
-    gpu.native.copy(kv.buf, b * Lmax * row, kvs[b].buf, 0, lens[b] * row);
+    gpu.op({ name: "copy", flops: 0 }, function () {
+      gpu.native.copy(kv.buf, b * Lmax * row, kvs[b].buf, 0, lens[b] * row);
+    });
   }
   var hostLens = Int32Array.from(lens);
   var keyLen = gpu.fromArray(hostLens, [B]);

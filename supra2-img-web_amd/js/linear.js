@@ -33,7 +33,7 @@ function linear(gpu, x, W, opts) {
   var act = ACT[o.act === undefined || o.act === null ? "none" : o.act];
   if (act === undefined) throw invalid("unknown act " + o.act);
   var out = o.out || gpu.empty([M, W.N]);
-  gpu.native.linear({
+  var args = {
     M: M,
     N: W.N,
     K: W.K,
@@ -46,6 +46,10 @@ function linear(gpu, x, W, opts) {
     gate: o.resid && o.gate ? raw(o.gate, "gate") : null,
     gateOff: o.gOff || 0,
     y: raw(out, "out"),
+  };
+  // flops 2*M*N*K, the reference's matmul meta (app/gpu/ops.js:15-31)
+  gpu.op({ name: "linear", flops: 2 * M * W.N * W.K }, function () {
+    gpu.native.linear(args);
   });
   return out;
 }

@@ -102,7 +102,10 @@ function attention(gpu, o) {
     args.workspaceBytes = wsBytes;
   }
   try {
-    gpu.native.attention(args);
+    // flops as the reference's profiler counts them (app/gpu/ops.js:116), over the B sequences
+    gpu.op({ name: "attention", flops: 4 * B * o.Lq * o.Lk * o.D * o.H }, function () {
+      gpu.native.attention(args);
+    });
   } finally {
     if (ws) ws.release();
   }
@@ -145,7 +148,9 @@ function relposBias(gpu, table, numBuckets, H, Lq, Lk, maxDistance) {
 function positionBias(gpu, table, numBuckets, H, L, maxDistance) {
   var rp = relposBias(gpu, table, numBuckets, H, L, L, maxDistance);
   var out = gpu.empty([H, L, L]);
-  gpu.native.positionBias(rp.table.buf, rp.lut.buf, numBuckets, H, L, L, out.buf);
+  gpu.op({ name: "positionBias", flops: 0 }, function () {
+    gpu.native.positionBias(rp.table.buf, rp.lut.buf, numBuckets, H, L, L, out.buf);
+  });
   if (rp.table !== table) rp.table.release();
   rp.lut.release();
   return out;

@@ -56,7 +56,11 @@ function attention(gpu, x, hw, A, opts) {
   args.workspace = ws.buf;
   args.workspaceBytes = bytes;
   try {
-    gpu.native.vaeAttention(args);
+    // q|k|v and output projections plus the attention (4 * HW^2 * C)
+    var flops = 2 * hw * 3 * C * C + 4 * hw * hw * C + 2 * hw * C * C;
+    gpu.op({ name: "vaeAttention", flops: flops }, function () {
+      gpu.native.vaeAttention(args);
+    });
   } finally {
     ws.release();  // stream-ordered pool reuse
   }

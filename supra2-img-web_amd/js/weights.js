@@ -127,7 +127,11 @@ SafeTensors.prototype._entry = function (name) {
 SafeTensors.prototype.decodeInto = function (gpu, name, dst, dstByteOffset) {
   var t = this._entry(name);
   var dev = this.resident(gpu);
-  this.native.toF32(dev.buf, t.data_offsets[0], this.codes[t.dtype], t.numel, dst, dstByteOffset || 0);
+  var native = this.native;
+  var code = this.codes[t.dtype];
+  this.gpu.op({ name: "toF32", flops: 0 }, function () {
+    native.toF32(dev.buf, t.data_offsets[0], code, t.numel, dst, dstByteOffset || 0);
+  });
   return t.numel;
 };
 
@@ -165,8 +169,15 @@ SafeTensors.prototype.rowsTensor = function (gpu, name, ids) {
   var out = g.empty([ids.length, dim]);
   if (ids.length) {
     var idt = g.fromArray(Int32Array.from(ids));
-    this.native.rowsF32(dev.buf, t.data_offsets[0], this.codes[t.dtype], t.shape[0], dim, idt.buf, ids.length, out.buf);
-    idt.release();
+    var native = this.native;
+    var code = this.codes[t.dtype];
+    try {
+      g.op({ name: "rowsF32", flops: 0 }, function () {
+        native.rowsF32(dev.buf, t.data_offsets[0], code, t.shape[0], dim, idt.buf, ids.length, out.buf);
+      });
+    } finally {
+      idt.release();
+    }
   }
   return out;
 };
@@ -245,7 +256,14 @@ function uploadConv3(gpu, src, base, cinPad) {
     var cp = cinPad || cin;
     var dev = src.resident(gpu);
     var buf = gpu.native.malloc(Math.max(16, cout * 9 * cp * 4));
-    gpu.native.conv3Pack(dev.buf, t.data_offsets[0], src.codes[t.dtype], cout, cin, cp, buf);
+    try {
+      gpu.op({ name: "conv3Pack", flops: 0 }, function () {
+        gpu.native.conv3Pack(dev.buf, t.data_offsets[0], src.codes[t.dtype], cout, cin, cp, buf);
+      });
+    } catch (e) {
+      gpu.native.free(buf);
+      throw e;
+    }
     var bias = src.has(base + "bias") ? persistent(gpu, src, base + "bias") : null;
     return Promise.resolve({ kind: "f32", N: cout, K: 9 * cp, buf: buf, bias: bias });
   } catch (e) {

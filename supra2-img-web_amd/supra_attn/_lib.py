@@ -49,6 +49,9 @@ SIGNATURES = {
     "sa_attention_f32": (c_int, [c_void_p, c_void_p]),
     "sa_attention_kernel_name": (c_char_p, [c_void_p]),
     "sa_attention_workspace_bytes": (c_int64, [c_void_p]),
+    "sa_attention_plan": (c_int, [c_void_p, c_void_p]),
+    "sa_attention_variant_count": (c_int32, []),
+    "sa_attention_variant": (c_int, [c_int32, c_void_p]),
     "sa_linear_f32": (c_int, [c_void_p, c_void_p]),
     "sa_linear_kernel_name": (c_char_p, [c_void_p]),
     "sa_vae_attention_f32": (c_int, [c_void_p, c_void_p]),
@@ -90,7 +93,13 @@ SIGNATURES = {
     "sa_conv3_pack_f32": (c_int, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p]),
     "sa_version": (c_int, []),
     "sa_last_error": (c_char_p, []),
+    "sa_last_status": (c_int, []),
 }
+
+SA_KERNEL_FLASH = 1
+SA_KERNEL_WIDE = 2
+SA_KERNEL_GENERIC = 3
+SA_MASK_VARIANT_KEY_LEN_SCHEDULED = 3
 
 
 class SaError(RuntimeError):
@@ -148,6 +157,32 @@ class AttnArgs(ctypes.Structure):
         self.struct_size = ctypes.sizeof(AttnArgs)
         for name, val in kw.items():
             setattr(self, name, val)
+
+
+class AttnPlan(ctypes.Structure):
+    """Mirror of sa_attn_plan (include/supra_attn.h)."""
+
+    _fields_ = [
+        ("struct_size", c_uint32),
+        ("kernel", c_int32),
+        ("head_dim", c_int32),
+        ("key_split", c_int32),
+        ("key_chunks", c_int32),
+        ("bias_mode", c_int32),
+        ("mask_variant", c_int32),
+        ("keys_per_step", c_int32),
+        ("workgroups", c_int64),
+        ("workspace_bytes", c_int64),
+        ("name", c_char_p),
+    ]
+
+    def __init__(self):
+        super().__init__()
+        self.struct_size = ctypes.sizeof(AttnPlan)
+
+    def variant(self) -> tuple:
+        """(kernel, head_dim, key_split, bias_mode, mask_variant): the compiled variant."""
+        return (self.kernel, self.head_dim, self.key_split, self.bias_mode, self.mask_variant)
 
 
 class LinearArgs(ctypes.Structure):
@@ -267,6 +302,24 @@ def kernel_name(args: AttnArgs) -> str:
     if name is None:
         raise SaError(-1, lib.sa_last_error().decode())
     return name.decode()
+
+
+def plan(args: AttnArgs) -> AttnPlan:
+    """The kernel variant, grid and workspace sa_attention_f32 would use for `args` (host only)."""
+    out = AttnPlan()
+    check(load().sa_attention_plan(ctypes.byref(args), ctypes.byref(out)))
+    return out
+
+
+def variants() -> list[AttnPlan]:
+    """Every compiled kernel variant (sa_attention_variant)."""
+    lib = load()
+    res = []
+    for i in range(lib.sa_attention_variant_count()):
+        v = AttnPlan()
+        check(lib.sa_attention_variant(i, ctypes.byref(v)))
+        res.append(v)
+    return res
 
 
 def linear(args: LinearArgs, stream: int | None = None) -> None:

@@ -227,6 +227,14 @@ function boundaryChecks(gpu) {
     code("SA_ERR_INVALID", /^y: 512 bytes at byte offset 0 lie outside the 504-byte buffer/));
   assert.throws(function () { n.linear({ M: 2, N: 64, K: 8, x: lx2, w: lw, y: ob }); },
     code("SA_ERR_INVALID", /^x: 64 bytes at byte offset 0 lie outside the 56-byte buffer/));
+  // a rejected call reports its own status, not a generic invalid-argument one
+  assert.throws(function () {
+    n.attention({ B: 1, H: 1, D: 64, Lq: 4, Lk: 4, q: kv, k: kv, v: kv, out: kv, ldq: 64, ldk: 64, ldv: 64, scale: 1 });
+  }, code("SA_ERR_ALIAS", /output overlaps q, k or v/));
+  assert.throws(function () {
+    n.kernelName({ B: 1, H: 1, D: 2048, Lq: 1, Lk: 1, q: qb, k: qb, v: qb, out: ob, ldq: 2048, ldk: 2048, ldv: 2048,
+                   scale: 1 });
+  }, code("SA_ERR_UNSUPPORTED", /head dim 2048 exceeds/));
   [qb, kv, ob, lx, lw, ly, lx2].forEach(function (b) { n.free(b); });
   var ev = n.eventCreate();
   n.eventDestroy(ev);

@@ -15,6 +15,7 @@ var device = require(path.join(root, "device.js"));
 var native = device.loadNative();
 
 var checks = 0;
+var pending = [];
 function check(name, fn) {
   fn();
   checks++;
@@ -26,7 +27,7 @@ check("addon exports", function () {
     "bucketLut", "positionBias", "eventCreate", "eventRecord", "eventElapsed", "eventDestroy"].forEach(function (f) {
     assert.strictEqual(typeof native[f], "function", f);
   });
-  assert.strictEqual(native.version(), 3);
+  assert.strictEqual(native.version(), 4);
   assert.strictEqual(native.SA_BIAS_RELPOS, 2);
   assert.strictEqual(native.SA_MASK_KEY_MASK, 2);
 });
@@ -348,7 +349,101 @@ check("released tensors are reused and cannot be passed again", function () {
   assert.strictEqual(device.BufferPool.round(5000), 5120);
 });
 
-var pending = [];
+// a fake addon with HIP events: elapsed time = difference of record counters (ms)
+function timedNative() {
+  var f = fakeNative();
+  var clock = 0, ev = 0;
+  f.created = 0;
+  f.destroyed = 0;
+  f.eventCreate = function () { f.created++; return { ev: ++ev, t: null }; };
+  f.eventRecord = function (e) { clock += 1; e.t = clock; };
+  f.eventElapsed = function (a, b) { return b.t - a.t; };
+  f.eventDestroy = function () { f.destroyed++; };
+  f.attention = function (a) { clock += 10; this.calls.push(a); };
+  f.linear = function (a) { clock += 100; this.lin.push(a); };
+  return f;
+}
+
+checkAsync("profiler: per-operator ms and flops (app/gpu/device.js:272-325)", function () {
+  var f = timedNative();
+  return device.GPU.create({ native: f, profile: true }).then(function (gpu) {
+    assert.ok(gpu.profiler instanceof device.Profiler);
+    var q = gpu.empty([256 * 2, 1728]);
+    sa.attention(gpu, { q: q, k: q, v: q, B: 2, Lq: 256, Lk: 256, H: 9, D: 64, ldq: 1728, ldk: 1728, ldv: 1728,
+                        kOff: 576, vOff: 1152, sq: 256 * 1728, sk: 256 * 1728, sv: 256 * 1728 });
+    sa.attention(gpu, { q: q, k: q, v: q, B: 2, Lq: 256, Lk: 256, H: 9, D: 64, ldq: 1728, ldk: 1728, ldv: 1728,
+                        kOff: 576, vOff: 1152, sq: 256 * 1728, sk: 256 * 1728, sv: 256 * 1728 });
+    var W = { kind: "f32", N: 1728, K: 576, buf: gpu.empty([1728, 576]), bias: null };
+    sa.linear(gpu, gpu.empty([512, 576]), W);
+    // a call rejected before its launch is not counted
+    f.attention = function () { var e = new Error("bad"); e.code = "SA_ERR_INVALID"; throw e; };
+    assert.throws(function () {
+      sa.attention(gpu, { q: q, k: q, v: q, Lq: 1, Lk: 1, H: 1, D: 64, ldq: 64, ldk: 64, ldv: 64 });
+    }, /bad/);
+    return gpu.profiler.report().then(function (rows) {
+      assert.strictEqual(rows.length, 2);
+      assert.strictEqual(rows[0].name, "linear");  // most time first
+      assert.strictEqual(rows[0].count, 1);
+      assert.strictEqual(rows[0].ms, 101);
+      assert.strictEqual(rows[0].flops, 2 * 512 * 1728 * 576);
+      assert.strictEqual(rows[1].name, "attention");
+      assert.strictEqual(rows[1].count, 2);
+      assert.strictEqual(rows[1].ms, 22);
+      assert.strictEqual(rows[1].flops, 2 * 4 * 2 * 256 * 256 * 64 * 9);  // 4 Lq Lk D H per sequence (ops.js:116)
+      gpu.profiler.reset();
+      return gpu.profiler.report();
+    }).then(function (rows) {
+      assert.strictEqual(rows.length, 0);
+      gpu.profiler.destroy();
+      assert.strictEqual(f.destroyed, f.created);  // events are recycled, then all destroyed
+      assert.strictEqual(f.created, 7);  // three timed calls + the start of the rejected one
+    });
+  });
+});
+
+checkAsync("device-lost latch: a HIP error makes every later call throw (app/gpu/device.js:134, 208)", function () {
+  var f = fakeNative();
+  var gpu = new device.GPU(f);
+  var q = gpu.empty([64, 64]);
+  var args = { q: q, k: q, v: q, Lq: 64, Lk: 64, H: 1, D: 64, ldq: 64, ldk: 64, ldv: 64 };
+  // an invalid-argument error does not mark the device lost
+  f.attention = function () { var e = new Error("bad stride"); e.code = "SA_ERR_INVALID"; throw e; };
+  assert.throws(function () { sa.attention(gpu, args); }, /bad stride/);
+  assert.strictEqual(gpu.lost, null);
+  f.attention = function () { var e = new Error("hipErrorLaunchFailure"); e.code = "SA_ERR_HIP"; throw e; };
+  assert.throws(function () { sa.attention(gpu, args); }, /hipErrorLaunchFailure/);
+  assert.ok(gpu.lost);
+  var launches = 0;
+  f.attention = function () { launches++; };
+  assert.throws(function () { sa.attention(gpu, args); }, function (e) {
+    return e.code === "SA_ERR_HIP" && /device lost: hipErrorLaunchFailure/.test(e.message);
+  });
+  assert.throws(function () { gpu.empty([4]); }, /device lost/);
+  assert.strictEqual(launches, 0);
+  // errors reported at sync latch too, and read/sync reject once lost
+  var g2 = new device.GPU(fakeNative());
+  g2.native.sync = function () { var e = new Error("async fault"); e.code = "SA_ERR_HIP"; throw e; };
+  return g2.sync().then(function () { assert.fail("sync resolved"); }, function (e) {
+    assert.ok(/async fault/.test(e.message));
+    assert.ok(g2.lost);
+    return gpu.read(q).then(function () { assert.fail("read resolved"); }, function (e2) {
+      assert.ok(/device lost/.test(e2.message));
+    });
+  });
+});
+
+check("fromArray checks the shape before taking a pooled buffer", function () {
+  var g = makeGpu();
+  assert.throws(function () { g.gpu.fromArray(new Float32Array(10), [3, 3]); }, /shape does not match/);
+  assert.strictEqual(g.f.mallocs, 0);
+  // an upload that fails returns its buffer to the pool
+  g.f.upload = function () { throw new Error("upload failed"); };
+  assert.throws(function () { g.gpu.fromArray(new Float32Array(10), [10]); }, /upload failed/);
+  g.f.upload = function () {};
+  var t = g.gpu.fromArray(new Float32Array(10), [2, 5]);
+  assert.strictEqual(g.f.mallocs, 1);
+  assert.deepStrictEqual(t.shape, [2, 5]);
+});
 
 function checkAsync(name, fn) {
   pending.push(function () {

@@ -20,6 +20,14 @@ HEADER = os.path.join(ROOT, "include", "supra_attn.h")
 HEADERS = [os.path.join(ROOT, "include", h) for h in sorted(os.listdir(os.path.join(ROOT, "include"))) if h.endswith(".h")]
 FAKE = 0x7F0000000000  # a device-looking address; validation only compares addresses
 
+# The tests that pass made-up addresses to the launching entry points (sa_attention_f32,
+# sa_linear_f32, sa_vae_attention_f32) to show that validation rejects a call before any launch run
+# only where no device is visible: on a GPU host a validation regression would launch a kernel on
+# those addresses. The host-only queries (sa_attention_plan, *_kernel_name, *_workspace_bytes) are
+# exercised everywhere.
+launches_fake_addresses = pytest.mark.skipif(_lib.device_count() > 0,
+                                             reason="made-up device addresses: run on a host without a GPU")
+
 
 def header_functions() -> list[str]:
     text = "\n".join(open(h).read() for h in HEADERS)
@@ -40,7 +48,7 @@ def test_every_declared_symbol_is_exported_and_bound():
 
 def test_version_and_constants():
     lib = _lib.load()
-    assert lib.sa_version() == 3
+    assert lib.sa_version() == 4
     text = open(HEADER).read()
     text += open(os.path.join(ROOT, "include", "supra_linear.h")).read()
     weights = open(os.path.join(ROOT, "include", "supra_weights.h")).read()
@@ -60,7 +68,8 @@ def test_version_and_constants():
 @pytest.mark.parametrize("cls,ctype,header", [(_lib.AttnArgs, "sa_attn_args", "supra_attn.h"),
                                               (_lib.LinearArgs, "sa_linear_args", "supra_linear.h"),
                                               (_lib.VaeAttnArgs, "sa_vae_attn_args", "supra_vae.h"),
-                                              (_lib.StTensor, "sa_st_tensor", "supra_weights.h")])
+                                              (_lib.StTensor, "sa_st_tensor", "supra_weights.h"),
+                                              (_lib.AttnPlan, "sa_attn_plan", "supra_attn.h")])
 def test_struct_layout_matches_c(tmp_path, cls, ctype, header):
     fields = [f[0] for f in cls._fields_]
     src = tmp_path / "layout.c"
@@ -142,6 +151,72 @@ def test_generic_kernel_for_other_head_dims_and_unaligned_rows():
     (dict(mask_mode=9), _lib.SA_ERR_INVALID),
     (dict(D=2048, ldq=1 << 16, ldk=1 << 16, ldv=1 << 16, ldo=1 << 16, so=256 << 16), _lib.SA_ERR_UNSUPPORTED),
 ])
+def test_plan_reports_the_rejection(over, code):
+    """The host-only plan query runs the same validation as the call and returns its status."""
+    args = good_args(**over)
+    if "struct_size" in over:
+        args.struct_size = over["struct_size"]
+    plan = _lib.AttnPlan()
+    lib = _lib.load()
+    assert lib.sa_attention_plan(ctypes.byref(args), ctypes.byref(plan)) == code
+    assert lib.sa_last_status() == code
+    assert lib.sa_attention_kernel_name(ctypes.byref(args)) is None
+    assert lib.sa_last_status() == code
+
+
+O = FAKE + (1 << 36)  # the output of the overlap cases below; q/k/v stay at FAKE
+
+
+@pytest.mark.parametrize("over", [
+    dict(bias_mode=1, bias=O + 1024),                                     # dense bias inside o
+    dict(bias_mode=1, bias=O - 4 * 9 * 256 * 256 + 4),                    # dense bias ending inside o
+    dict(bias_mode=1, bias=O - 4 * 9 * 256 * 256 - 1024, sbias=9 * 256 * 256),  # second batch's bias inside o
+    dict(bias_mode=2, bias=O + 64, bucket_lut=FAKE + (3 << 36), num_buckets=32),   # relpos table
+    dict(bias_mode=2, bias=FAKE + (3 << 36), bucket_lut=O + 64, num_buckets=32),   # bucket LUT
+    dict(mask_mode=1, key_len=O + 4),                                     # key lengths
+    dict(mask_mode=2, key_mask=O + 100),                                  # key mask
+    dict(mask_mode=2, key_mask=O - 256 - 10, smask=256),                  # the second sequence's mask row
+])
+def test_output_overlapping_any_read_operand_is_an_alias(over):
+    args = good_args(o=O, **over)
+    plan = _lib.AttnPlan()
+    assert _lib.load().sa_attention_plan(ctypes.byref(args), ctypes.byref(plan)) == _lib.SA_ERR_ALIAS
+    assert b"overlaps" in _lib.load().sa_last_error()
+    # the same operands clear of o are accepted
+    moved = {k: (v + (1 << 38) if k in ("bias", "bucket_lut", "key_len", "key_mask") else v) for k, v in over.items()}
+    assert _lib.plan(good_args(o=O, **moved)).name
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(struct_size=8), _lib.SA_ERR_INVALID),
+    (dict(B=0), _lib.SA_ERR_INVALID),
+    (dict(H=0), _lib.SA_ERR_INVALID),
+    (dict(Lq=0), _lib.SA_ERR_INVALID),
+    (dict(Lk=0), _lib.SA_ERR_INVALID),
+    (dict(q=0), _lib.SA_ERR_INVALID),
+    (dict(o=0), _lib.SA_ERR_INVALID),
+    (dict(scale=float("nan")), _lib.SA_ERR_INVALID),
+    (dict(scale=float("inf")), _lib.SA_ERR_INVALID),
+    (dict(q_off=-4), _lib.SA_ERR_INVALID),
+    (dict(ldq=500), _lib.SA_ERR_INVALID),
+    (dict(ldo=100), _lib.SA_ERR_INVALID),
+    (dict(so=100), _lib.SA_ERR_INVALID),
+    (dict(sq=-1), _lib.SA_ERR_INVALID),
+    (dict(k_off=1 << 40), _lib.SA_ERR_INVALID),
+    (dict(ldv=1 << 41), _lib.SA_ERR_INVALID),
+    (dict(sk=1 << 40), _lib.SA_ERR_INVALID),
+    (dict(o=FAKE + 4096), _lib.SA_ERR_ALIAS),
+    (dict(bias_mode=1), _lib.SA_ERR_INVALID),
+    (dict(bias_mode=2, bias=FAKE + (2 << 32)), _lib.SA_ERR_INVALID),
+    (dict(bias_mode=2, bias=FAKE + (2 << 32), bucket_lut=FAKE + (3 << 32)), _lib.SA_ERR_INVALID),
+    (dict(bias_mode=7), _lib.SA_ERR_INVALID),
+    (dict(mask_mode=1), _lib.SA_ERR_INVALID),
+    (dict(mask_mode=2), _lib.SA_ERR_INVALID),
+    (dict(mask_mode=2, key_mask=FAKE + (2 << 32), smask=100), _lib.SA_ERR_INVALID),
+    (dict(mask_mode=9), _lib.SA_ERR_INVALID),
+    (dict(D=2048, ldq=1 << 16, ldk=1 << 16, ldv=1 << 16, ldo=1 << 16, so=256 << 16), _lib.SA_ERR_UNSUPPORTED),
+])
+@launches_fake_addresses
 def test_invalid_calls_are_rejected_before_launch(over, code):
     args = good_args(**over)
     if "struct_size" in over:
@@ -168,6 +243,7 @@ def test_revision2_struct_size_is_accepted():
     assert _lib.load().sa_attention_kernel_name(ctypes.byref(args)) is None
 
 
+@launches_fake_addresses
 def test_extents_that_overflow_are_rejected():
     """Offsets and strides below the 2^40 limit can still multiply past int64 with a large batch or
     row count: the extent arithmetic is checked, and such calls fail with a message that says so."""
@@ -181,12 +257,14 @@ def test_extents_that_overflow_are_rejected():
     assert b"overflows" in lib.sa_last_error()
 
 
+@launches_fake_addresses
 def test_null_args_pointer():
     lib = _lib.load()
     assert lib.sa_attention_f32(None, None) == _lib.SA_ERR_INVALID
     assert b"NULL" in lib.sa_last_error()
 
 
+@launches_fake_addresses
 def test_error_message_clears_on_success():
     lib = _lib.load()
     assert rc_of(good_args(B=0)) == _lib.SA_ERR_INVALID
@@ -255,6 +333,7 @@ def test_workspace_size_query():
     (dict(workspace=FAKE + (3 << 24) - 64, workspace_bytes="need"), _lib.SA_ERR_ALIAS, "overlaps"),
     (dict(workspace=FAKE + (1 << 24) + 4096, workspace_bytes="need"), _lib.SA_ERR_ALIAS, "overlaps"),
 ])
+@launches_fake_addresses
 def test_workspace_is_checked_before_launch(over, code, text):
     need = _lib.workspace_bytes(vae_args())
     over = {k: (need - 1 if v == "need-1" else need if v == "need" else v) for k, v in over.items()}
@@ -308,6 +387,7 @@ def test_linear_kernel_choice():
     (dict(epilogue=2, gate=FAKE + (2 << 30), gate_off=8), _lib.SA_ERR_ALIAS),
     (dict(M=2000000, K=36, w=FAKE + (1 << 40), y=FAKE + (2 << 40), bias=0), _lib.SA_ERR_UNSUPPORTED),
 ])
+@launches_fake_addresses
 def test_invalid_linear_calls_are_rejected(over, code):
     args = lin_args(**over)
     if "struct_size" in over:
@@ -347,6 +427,7 @@ def test_vae_workspace_size():
     (dict(out=FAKE + (2 << 30)), _lib.SA_ERR_ALIAS),               # out over the weights
     (dict(workspace=FAKE + (4 << 30) + 1024), _lib.SA_ERR_ALIAS),  # workspace over out
 ])
+@launches_fake_addresses
 def test_invalid_vae_calls_are_rejected(over, code):
     args = vae_block_args(**over)
     if "struct_size" in over:

@@ -1,0 +1,115 @@
+"""One attention call per compiled flash-kernel variant <D, key_split, bias, mask>.
+
+Each call has the shape real callers give that variant (T5 batches with the relative-position
+bias, DiT-sized batches, head dim 128 with every bias and mask), ragged Lq and Lk (not multiples
+of 32), and enough keys that every splitting wave runs at least two loop steps, so the second LDS
+stage of the K/V, relative-bias and key-mask staging is read and the softmax reference is carried
+across blocks. The kernel choice is the library's own (sa_attention_plan); the shapes below are
+picked so that it lands on the wanted variant, which tests assert.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from supra_attn import _lib
+from cases import make_call
+
+# (D, key_split) -> (B, H, Lq, Lk): every B >= 8 (the scheduled key-length variant needs it), and
+# ceil(Lk / 32) >= 2 * key_split (at least two steps for the last splitting wave).
+SHAPES = {
+    (64, 1): (48, 12, 123, 123),   # T5-like batch of prompts (48 x 12 heads, 4 query tiles of 128)
+    (64, 2): (16, 12, 200, 150),
+    (64, 4): (8, 4, 100, 250),
+    (128, 1): (32, 8, 250, 100),   # head dim 128 (the reference's fused gate admits it, ops.js:112)
+    (128, 2): (8, 2, 100, 150),
+}
+
+MASK_NAMES = {0: "none", 1: "key_len", 2: "key_mask", 3: "key_len_scheduled"}
+BIAS_NAMES = {0: "none", 1: "dense", 2: "relpos"}
+
+
+def key_lengths(rng, B: int, Lk: int, split: int) -> np.ndarray:
+    """Mostly long sequences (two steps or more per splitting wave), plus a ragged short one, a
+    zero and a full one; not sorted, so the longest-first schedule is not the identity."""
+    lo = 32 * (2 * split - 1) + 1  # last splitting wave still gets two blocks
+    kl = rng.integers(min(lo, Lk), Lk + 1, size=B).astype(np.int32)
+    kl[1] = Lk
+    kl[2] = 0
+    kl[3] = 5
+    return kl
+
+
+def call_for(D: int, split: int, bias: int, mask: int, seed: int = 0):
+    """(call, host_key_len) for the variant; host_key_len says whether the host copy of the key
+    lengths goes with the call (it selects the scheduled variant)."""
+    B, H, Lq, Lk = SHAPES[(D, split)]
+    seed = seed + 1000 * D + 100 * split + 10 * bias + mask
+    rng = np.random.default_rng(seed)
+    mask_mode = {0: _lib.SA_MASK_NONE, 1: _lib.SA_MASK_KEY_LEN, 2: _lib.SA_MASK_KEY_MASK,
+                 3: _lib.SA_MASK_KEY_LEN}[mask]
+    kl = key_lengths(rng, B, Lk, split) if mask_mode == _lib.SA_MASK_KEY_LEN else None
+    # T5 calls carry no 1/sqrt(d) scaling (t5.js:80); the others the ops.js default
+    scale = 1.0 if bias == _lib.SA_BIAS_RELPOS else None
+    call = make_call(B=B, H=H, D=D, Lq=Lq, Lk=Lk, seed=seed, scale=scale, packed=(D == 64 and bias == 0),
+                     bias_mode=bias, mask_mode=mask_mode, key_len=kl,
+                     dense_bias_batched=(bias == _lib.SA_BIAS_DENSE and split == 1),
+                     name=f"flash_d{D}_s{split}_{BIAS_NAMES[bias]}_{MASK_NAMES[mask]}")
+    if mask_mode == _lib.SA_MASK_KEY_MASK:
+        call.key_mask[0, :] = 0  # a sequence with no attended key: zeros
+    return call, mask == 3
+
+
+def fake_args(call, host_key_len: bool) -> _lib.AttnArgs:
+    """sa_attn_args for `call` with distinct, 16-byte aligned made-up device addresses: enough for
+    the host-only plan query (which compares addresses but never dereferences them)."""
+    base = [0x7F0000000000]
+
+    def addr(nbytes):
+        a = base[0]
+        base[0] += (int(nbytes) + 4095) // 4096 * 4096 + 4096
+        return a
+
+    q = addr(call.q.nbytes)
+    k = q if call.same_qkv else addr(call.k.nbytes)
+    v = q if call.same_qkv else addr(call.v.nbytes)
+    kw = dict(B=call.B, H=call.H, D=call.D, Lq=call.Lq, Lk=call.Lk, q=q, k=k, v=v,
+              o=addr(4 * int(np.prod(call.out_shape))), scale=call.scale, bias_mode=call.bias_mode,
+              mask_mode=call.mask_mode)
+    kw.update(call.args)
+    keep = []
+    if call.bias is not None:
+        kw["bias"] = addr(call.bias.nbytes)
+    if call.lut is not None:
+        kw["bucket_lut"] = addr(4 * len(call.lut))
+        kw["num_buckets"] = int(call.bias.shape[0])
+    if call.key_len is not None:
+        kw["key_len"] = addr(call.key_len.nbytes)
+        if host_key_len:
+            kl = np.ascontiguousarray(call.key_len, dtype=np.int32)
+            keep.append(kl)
+            kw["key_len_host"] = kl.ctypes.data
+    if call.key_mask is not None:
+        kw["key_mask"] = addr(call.key_mask.nbytes)
+        kw.setdefault("smask", call.key_mask.shape[-1])
+    args = _lib.AttnArgs(**kw)
+    args._keep = keep  # the host key lengths must outlive the query
+    return args
+
+
+def flash_variants() -> list[tuple]:
+    """(D, key_split, bias, mask) of every compiled flash variant."""
+    return [(v.head_dim, v.key_split, v.bias_mode, v.mask_variant) for v in _lib.variants()
+            if v.kernel == _lib.SA_KERNEL_FLASH]
+
+
+def min_steps_per_wave(call, split: int) -> int:
+    """Loop steps of the busiest splitting wave of the longest sequence (key blocks of 32)."""
+    if call.key_len is not None:
+        kv = int(np.clip(call.key_len, 0, call.Lk).max())
+    else:
+        kv = call.Lk
+    nblk = (kv + 31) // 32
+    return (nblk - (split - 1) + split - 1) // split  # blocks of the last splitting wave
