@@ -116,6 +116,21 @@ typedef struct sa_attn_args {
  * per-sample host loops of app/models/dit.js:170-185 into one launch. Asynchronous on `stream`. */
 int sa_attention_f32(const sa_attn_args* args, void* stream);
 
+/* Scratch the allocation-free entry point has per GPU: 32 MiB of device memory, held from the
+ * library's first such call on that GPU until the process ends. */
+#define SA_NOALLOC_SCRATCH_BYTES (32 << 20)
+
+/* sa_attention_f32 for callers that cannot allocate device memory: code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc. No counterpart in the reference.
+ * args->workspace and workspace_bytes are ignored: the kernels that merge partial results across
+ * workgroups use the library's own per-GPU scratch (a static device array of
+ * SA_NOALLOC_SCRATCH_BYTES), and a call that needs more (sa_attention_workspace_bytes) fails with
+ * SA_ERR_UNSUPPORTED before any launch. Nothing in the call allocates (the first call on a GPU
+ * looks up that GPU's scratch address, once). Every call on one GPU shares its scratch: calls
+ * ordered on one stream are fine, calls that overlap on one GPU (other streams, other threads)
+ * race. The scratch holds nothing that must start at zero. */
+int sa_attention_f32_noalloc(const sa_attn_args* args, void* stream);
+
 /* Device scratch bytes sa_attention_f32 needs for these arguments on the current device (0 for
  * most calls; the wide-head kernel splits long key ranges across workgroups and merges their
  * partial results through it), or a negative SA_ERR_* status if the arguments are rejected.

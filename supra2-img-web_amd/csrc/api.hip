@@ -390,7 +390,36 @@ int choose(const sa::AttnParams& p, Choice* c) {
 
 extern "C" {
 
-int sa_attention_f32(const sa_attn_args* args, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// ---- scratch of the allocation-free entry point: one static device array, which every GPU the
+// library runs on holds (its own copy, at its own address) until the process ends. In host code
+// `scratch` names a host-side stand-in, never the device memory: host code uses only the address
+// hipGetSymbolAddress returns for the current device (kept per device in g_scratch).
+constexpr int64_t kScratchBytes = SA_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+std::atomic<void*> g_scratch[kMaxDevices];
+
+// Device address of the current device's scratch, looked up on the first call on that device.
+int scratch_address(void** out) {
+  const int dev = current_device();
+  if (dev < 0) return fail(SA_ERR_HIP, "no current HIP device");
+  void* ptr = g_scratch[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (ptr == nullptr) return fail(SA_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch[dev].store(ptr, std::memory_order_release);
+  }
+  *out = ptr;
+  return SA_OK;
+}
+
+// Validates, selects and launches one attention call. The wide-head kernel's merge records go to
+// the caller's workspace, or (own_scratch) to the library's per-GPU scratch.
+int run_attention(const sa_attn_args* args, void* stream, bool own_scratch) {
   sa::AttnParams p;
   int rc = resolve(args, &p);
   if (rc != SA_OK) return rc;
@@ -404,18 +433,30 @@ int sa_attention_f32(const sa_attn_args* args, void* stream) {
     float* ws = nullptr;
     if (c.wide.ws_floats > 0) {
       const int64_t need = c.wide.ws_floats * (int64_t)sizeof(float);
-      if (!args->workspace || args->workspace_bytes < need)
-        return fail(SA_ERR_INVALID, "this call needs a device workspace of %lld bytes (sa_attention_workspace_bytes)",
-                    (long long)need);
-      if (!aligned16(args->workspace)) return fail(SA_ERR_INVALID, "workspace must be 16-byte aligned");
-      const Extent ew = {(uintptr_t)args->workspace, (uintptr_t)args->workspace + (uintptr_t)need, true};
+      void* base = nullptr;
+      if (own_scratch) {
+        if (need > kScratchBytes)
+          return fail(SA_ERR_UNSUPPORTED,
+                      "this call needs %lld bytes of scratch, more than the %lld bytes sa_attention_f32_noalloc has "
+                      "(pass a workspace to sa_attention_f32 instead)",
+                      (long long)need, (long long)kScratchBytes);
+        rc = scratch_address(&base);
+        if (rc != SA_OK) return rc;
+      } else {
+        if (!args->workspace || args->workspace_bytes < need)
+          return fail(SA_ERR_INVALID, "this call needs a device workspace of %lld bytes (sa_attention_workspace_bytes)",
+                      (long long)need);
+        if (!aligned16(args->workspace)) return fail(SA_ERR_INVALID, "workspace must be 16-byte aligned");
+        base = args->workspace;
+      }
+      const Extent ew = {(uintptr_t)base, (uintptr_t)base + (uintptr_t)need, true};
       const int64_t HD = (int64_t)p.H * p.D;
       if (overlaps(ew, extent(p.o, p.o_off, p.so, p.ldo, p.B, p.Lq, HD)) ||
           overlaps(ew, extent(p.q, p.q_off, p.sq, p.ldq, p.B, p.Lq, HD)) ||
           overlaps(ew, extent(p.k, p.k_off, p.sk, p.ldk, p.B, p.Lk, HD)) ||
           overlaps(ew, extent(p.v, p.v_off, p.sv, p.ldv, p.B, p.Lk, HD)))
         return fail(SA_ERR_ALIAS, "the workspace overlaps q, k, v or o");
-      ws = static_cast<float*>(args->workspace);
+      ws = static_cast<float*>(base);
     }
     e = sa::launch_wide_mfma(p, c.wide, ws, (hipStream_t)stream);
   } else {
@@ -424,6 +465,14 @@ int sa_attention_f32(const sa_attn_args* args, void* stream) {
   if (e != hipSuccess) return hip_fail(e, c.name);
   return ok();
 }
+
+}  // namespace
+
+extern "C" {
+
+int sa_attention_f32(const sa_attn_args* args, void* stream) { return run_attention(args, stream, false); }
+
+int sa_attention_f32_noalloc(const sa_attn_args* args, void* stream) { return run_attention(args, stream, true); }
 
 int64_t sa_attention_workspace_bytes(const sa_attn_args* args) {
   sa::AttnParams p;

@@ -47,6 +47,7 @@ SA_ST_MAX_DIMS = 8
 # Every symbol include/*.h declares, with (restype, argtypes).
 SIGNATURES = {
     "sa_attention_f32": (c_int, [c_void_p, c_void_p]),
+    "sa_attention_f32_noalloc": (c_int, [c_void_p, c_void_p]),
     "sa_attention_kernel_name": (c_char_p, [c_void_p]),
     "sa_attention_workspace_bytes": (c_int64, [c_void_p]),
     "sa_attention_plan": (c_int, [c_void_p, c_void_p]),
@@ -95,6 +96,8 @@ SIGNATURES = {
     "sa_last_error": (c_char_p, []),
     "sa_last_status": (c_int, []),
 }
+
+SA_NOALLOC_SCRATCH_BYTES = 32 << 20
 
 SA_KERNEL_FLASH = 1
 SA_KERNEL_WIDE = 2

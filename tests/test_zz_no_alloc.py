@@ -1,0 +1,89 @@
+"""sa_attention_f32_noalloc, the allocation-free entry point, against sa_attention_f32 with a
+caller workspace: the same kernels, so bit for bit the same outputs, and both within the parity bar
+of the PyTorch fp32 CPU path. Two calls in a row on the library's per-GPU scratch, the second one
+smaller, then a flash call (no scratch) and a call whose scratch would exceed the limit (rejected
+before any launch)."""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import attention as orc
+from supra_attn import _lib, workloads
+from supra_attn.runner import Staged
+from cases import make_call
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+def run_both(dev, call):
+    """Outputs of sa_attention_f32 (workspace from the caller) and sa_attention_f32_noalloc (no
+    workspace fields set) on the same device-resident inputs."""
+    print(f"[case] noalloc {call.name} B={call.B} H={call.H} D={call.D} Lq={call.Lq} Lk={call.Lk}", flush=True)
+    lib = _lib.load()
+    st = Staged(dev, call, out_fill=np.float32(-7.0))
+    try:
+        need = _lib.workspace_bytes(st.args)
+        st.launch()
+        dev.sync()
+        ref = st.out.read()
+        st.out.upload(np.full(call.out_shape, np.float32(-7.0), dtype=np.float32))
+        args = _lib.AttnArgs()
+        ctypes.memmove(ctypes.byref(args), ctypes.byref(st.args), ctypes.sizeof(args))
+        args.workspace = None
+        args.workspace_bytes = 0
+        _lib.check(lib.sa_attention_f32_noalloc(ctypes.byref(args), ctypes.c_void_p(dev.stream)))
+        dev.sync()
+        got = st.out.read()
+    finally:
+        st.release()
+    return ref, got, need
+
+
+def check_case(dev, call):
+    ref, got, need = run_both(dev, call)
+    assert np.array_equal(ref.view(np.uint32), got.view(np.uint32)), f"{call.name}: noalloc differs from the workspace call"
+    e = orc.errors(orc.output_view(got, call), orc.reference_torch(call))
+    assert e["finite"] and e["rel_l2"] <= TOL and e["max_rel"] <= TOL, f"{call.name}: {e}"
+    return need
+
+
+def test_noalloc_matches_the_workspace_call_twice_then_smaller(dev):
+    # the VAE mid-block shape: the wide-head kernel merges 8 key chunks through the scratch
+    need1 = check_case(dev, workloads.vae_mid(seed=3))
+    assert 0 < need1 <= _lib.SA_NOALLOC_SCRATCH_BYTES
+    # a smaller call right after, on the same scratch (ragged, fewer query groups and key chunks)
+    need2 = check_case(dev, make_call(B=1, H=1, D=512, Lq=700, Lk=650, seed=41))
+    assert 0 < need2 < need1
+    # a head-dim-256 call with key lengths
+    check_case(dev, make_call(B=2, H=1, D=256, Lq=300, Lk=520, mask_mode=_lib.SA_MASK_KEY_LEN, key_len=[520, 77],
+                              seed=42))
+
+
+def test_noalloc_flash_call_needs_no_scratch(dev):
+    need = check_case(dev, workloads.dit_self(B=2, seed=0))
+    assert need == 0
+
+
+def test_noalloc_rejects_calls_beyond_its_scratch(dev):
+    """511 query groups of a head-dim-256 head, each split in two key chunks: 33.75 MB of merge
+    records, more than the 32 MiB scratch. Rejected on the host, before any launch."""
+    lib = _lib.load()
+    Lq, D = 511 * 32, 256
+    q = dev.empty((Lq * D,))
+    o = dev.empty((Lq * D,))
+    try:
+        args = _lib.AttnArgs(B=1, H=1, D=D, Lq=Lq, Lk=64, q=q.ptr, k=q.ptr, v=q.ptr, o=o.ptr, ldq=D, ldk=D, ldv=D,
+                             scale=1.0 / 16)
+        assert _lib.workspace_bytes(args) > _lib.SA_NOALLOC_SCRATCH_BYTES
+        rc = lib.sa_attention_f32_noalloc(ctypes.byref(args), ctypes.c_void_p(dev.stream))
+        assert rc == _lib.SA_ERR_UNSUPPORTED
+        assert b"scratch" in lib.sa_last_error()
+    finally:
+        q.release()
+        o.release()
