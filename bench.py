@@ -47,13 +47,27 @@ def log(msg: str) -> None:
     sys.stderr.flush()
 
 
-def time_calls(dev, launch, n: int, warmup: int) -> float:
-    """Average ms per call of `launch` over n back-to-back calls on the device stream."""
-    from supra_attn.device import Event
+MIN_WARMUP_S = 0.05  # the GPU clocks take about 25 ms of load to settle; every timing warms up at least this long
 
-    for _ in range(warmup):
+
+def warm(dev, launch, calls: int, seconds: float = MIN_WARMUP_S) -> None:
+    """At least `calls` calls and at least `seconds` of device time of back-to-back calls."""
+    for _ in range(calls):
         launch()
     dev.sync()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(4):
+            launch()
+        dev.sync()
+
+
+def time_calls(dev, launch, n: int, warmup: int) -> float:
+    """Average ms per call of `launch` over n back-to-back calls on the device stream, after a
+    warm-up of `warmup` calls and at least MIN_WARMUP_S of calls."""
+    from supra_attn.device import Event
+
+    warm(dev, launch, warmup)
     e0, e1 = Event(), Event()
     e0.record(dev.stream)
     for _ in range(n):
@@ -63,15 +77,49 @@ def time_calls(dev, launch, n: int, warmup: int) -> float:
     return e0.elapsed_ms(e1) / n
 
 
+def kernel_sources_digest() -> str:
+    """sha256 of every kernel and C ABI source (csrc/*.hip, csrc/*.h, include/*.h), in name order:
+    the counter figures in profiles/hbm_traffic.json hold only for the sources they were measured on."""
+    import hashlib
+
+    h = hashlib.sha256()
+    csrc = os.path.join(PKG, "csrc")
+    inc = os.path.join(ROOT, "include")
+    files = sorted(os.path.join(csrc, f) for f in os.listdir(csrc) if f.endswith((".hip", ".h")))
+    files += sorted(os.path.join(inc, f) for f in os.listdir(inc) if f.endswith(".h"))
+    for path in files:
+        h.update(os.path.basename(path).encode() + b"\0")
+        with open(path, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
 def traffic_from_profiles(workload: str):
     """HBM bytes per launch of `workload`'s kernel from the committed rocprofv3 counter summary
-    (FETCH_SIZE and WRITE_SIZE passes scaled by a 256 MiB copy), if present."""
+    (FETCH_SIZE and WRITE_SIZE passes scaled by a 256 MiB copy), or None when there is none for the
+    current kernel sources (the summary's source digest differs: the kernels changed since)."""
     path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
     try:
         with open(path) as f:
-            return json.load(f).get(workload, {}).get("bytes_per_launch")
+            data = json.load(f)
     except (OSError, ValueError):
         return None
+    if data.get("sources_sha256") != kernel_sources_digest():
+        log("profiles/hbm_traffic.json was measured on other kernel sources: traffic reported as null")
+        return None
+    return data.get(workload, {}).get("bytes_per_launch")
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or the platform's processor string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def cpu_baseline(data, seconds: float) -> dict:
@@ -104,10 +152,11 @@ def cpu_baseline(data, seconds: float) -> dict:
         "value": flops * steps / dt / 1e12,
         "unit": "TFLOP/s",
         "cores": threads,
+        "cpu_model": cpu_model(),
         "kind": "port",
         "sample": f"{steps} of the sweep's denoising steps ({28 * steps} calls: 14 blocks x self+cross, batch 64) "
                   f"with torch {torch.__version__} F.scaled_dot_product_attention on the CPU "
-                  f"({os.cpu_count()} logical CPUs visible, {threads} threads, {platform.processor() or platform.machine()}); "
+                  f"({os.cpu_count()} logical CPUs visible, {threads} threads, {cpu_model()}); "
                   f"{dt:.2f} s, {dt / steps * 1e3:.1f} ms/step",
         "ms_per_step": dt / steps * 1e3,
     }
@@ -447,7 +496,7 @@ def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=20)  # ~40 ms: the clocks settle after ~25 ms of load
+    ap.add_argument("--warmup", type=int, default=20)  # plus at least MIN_WARMUP_S of steps: the clocks settle after ~25 ms
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calls", type=int, default=200, help="calls per single-config timing")
@@ -485,9 +534,7 @@ def main() -> int:
             s.launch()
             c.launch()
 
-    for _ in range(args.warmup):
-        step()
-    dev.sync()
+    warm(dev, step, args.warmup)  # --warmup steps, and at least MIN_WARMUP_S of them
     e0, e1 = Event(), Event()
     e0.record(dev.stream)
     for _ in range(args.steps):
@@ -608,6 +655,7 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_TFLOPS, 4),
             "traffic": traffic_from_profiles("sweep_self"),
+            "traffic_sources_sha256": kernel_sources_digest(),
             "algorithmic_flops_per_launch": self_flops,
             "algorithmic_bytes_per_launch": self_call.algorithmic_bytes(),
             "us_per_launch": round(self_ms * 1e3, 3),
