@@ -26,11 +26,15 @@ __device__ __forceinline__ int xcd_remap(int bid, int n) {
   return xcd < r ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
 }
 
+// IEEE 754-2019 maximum (a NaN operand gives NaN): one v_maximum3_f32 per two new operands on gfx950,
+// where fmaxf also canonicalizes its operands. A NaN score ends in a NaN output either way.
+__device__ __forceinline__ float max_nan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 // Exchange with the lane 32 away (v_permlane32_swap): returns {own, partner} in some order, so
 // symmetric reductions (max, +) can combine the two results directly.
 __device__ __forceinline__ float max_with_partner(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return max_nan(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float sum_with_partner(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);

@@ -54,6 +54,8 @@
 //   V: chunk c of row r at c ^ (8 * ((r >> 2) & 1)), so the two half-waves (rows 4 apart) read
 //      disjoint bank halves.
 
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -235,8 +237,11 @@ __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void
   }
 
 
-  for (int step = 0; step < nstep; ++step) {
-    const int buf = step & 1;
+  // One loop step on LDS stage `stage`: a compile-time constant in the single-split kernels (two
+  // steps per iteration, so every LDS address of a step is a base register plus an immediate
+  // offset), a run-time value in the key-split kernels, whose loops run one to a few steps.
+  auto step_body = [&](int step, auto stage) {
+    const int buf = stage;
     // stage `buf` has landed for this thread; the barrier makes it whole, and every wave has
     // finished reading stage buf^1 (the previous step), which the next issue (from step 1 on:
     // step 1 itself was issued before the loop) overwrites
@@ -316,10 +321,10 @@ __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void
       // ---- online softmax with a lazily moved reference
       float mb = u[0];
 #pragma unroll
-      for (int r = 1; r < 16; ++r) mb = fmaxf(mb, u[r]);
+      for (int r = 1; r < 16; ++r) mb = max_nan(mb, u[r]);
       mb = max_with_partner(mb);
       if (__builtin_amdgcn_ballot_w64(mb > m + kRescaleSlack) != 0) {
-        const float m_new = fmaxf(m, mb);
+        const float m_new = max_nan(m, mb);
         const float alpha = fast_exp2(m - m_new);
         m = m_new;
         l *= alpha;
@@ -349,6 +354,17 @@ __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void
         }
       }
     }
+  };
+  if constexpr (NSPLIT == 1) {
+    int step = 0;
+    for (; step + 1 < nstep; step += 2) {
+      step_body(step, std::integral_constant<int, 0>{});
+      step_body(step + 1, std::integral_constant<int, 1>{});
+    }
+    if (step < nstep) step_body(step, std::integral_constant<int, 0>{});
+  } else {
+    // the key-split kernels run one to a few steps: one copy of the body, stage chosen at run time
+    for (int step = 0; step < nstep; ++step) step_body(step, step & 1);
   }
 
   // ---- merge the key splits: waves ks > 0 publish (O, m, l), wave ks == 0 combines

@@ -3,20 +3,21 @@
 // unfused GEMM -> softmax -> GEMM path (app/gpu/ops.js:119-147).
 //
 // Work decomposition
-//   One workgroup = 4 wave64s = 32 queries x one chunk of keys. Wave w owns the head-dim slice
-//   [w*D/4, (w+1)*D/4) of Q, K, V and O: per 32-key block it computes the partial score tile
-//   S_w^T = K_w Q_w^T over its slice (v_mfma_f32_32x32x2f32, the same transposed layout as the
-//   flash kernel), the four partial tiles are summed through LDS in a fixed order (so every wave
-//   derives bit-identical probabilities), and each wave accumulates O_w^T += V_w^T P^T for its
-//   slice. K and V slices are private to their wave: each wave streams its own slice into LDS
-//   with global_load_lds_dwordx4, and only the score exchange needs workgroup barriers.
+//   One workgroup = NW wave64s = 32 queries x one chunk of keys (NW = 8 for D = 512: two waves per
+//   SIMD; 4 for D = 256). Wave w owns the head-dim slice [w*D/NW, (w+1)*D/NW) of Q, K, V and O:
+//   per 32-key block it computes the partial score tile S_w^T = K_w Q_w^T over its slice
+//   (v_mfma_f32_32x32x2f32, the same transposed layout as the flash kernel), the NW partial tiles
+//   are summed through LDS in two stages in a fixed order (so every wave derives bit-identical
+//   probabilities), and each wave accumulates O_w^T += V_w^T P^T for its slice. K and V slices are
+//   private to their wave: each wave streams its own slice into LDS with global_load_lds_dwordx4,
+//   and only the score exchange needs workgroup barriers.
 //   One head of 1024 queries gives just 32 query groups, so the keys are also split across
 //   workgroups (nks chunks). Each workgroup writes its partial (O, m, l) to a workspace and a
 //   second, fully parallel kernel merges the chunks of every query group with the online-softmax
 //   rescale (the kernel boundary orders the two; no atomics or cross-XCD fences).
 //
-// LDS per workgroup: K and V slices [32 keys][D/4] per wave (XOR-swizzled as in the flash kernel)
-// plus the score exchange: 144 KiB for D = 512 (one workgroup per CU), 80 KiB for D = 256.
+// LDS per workgroup: K and V slices [32 keys][D/NW] per wave (XOR-swizzled as in the flash kernel)
+// plus the score exchange: 160 KiB for D = 512 (one workgroup per CU), 80 KiB for D = 256.
 
 #include <algorithm>
 
@@ -37,9 +38,9 @@ __device__ __forceinline__ f32x16 zero16() {
   return z;
 }
 
-template <int D, int MASK>
-__global__ __launch_bounds__(256, 1) void wide_mfma_kernel(AttnParams p, int q_groups, int nks, int chunk, float* ws) {
-  constexpr int DS = D / 4;       // head dims per wave
+template <int D, int NW, int MASK>
+__global__ __launch_bounds__(64 * NW, 1) void wide_mfma_kernel(AttnParams p, int q_groups, int nks, int chunk, float* ws) {
+  constexpr int DS = D / NW;      // head dims per wave
   constexpr int QREG = DS / 2;    // Q values per lane
   constexpr int NDB = DS / 32;    // 32-dim output tiles per wave
   constexpr int CPR = DS / 4;     // 16-byte chunks per slice row
@@ -50,9 +51,9 @@ __global__ __launch_bounds__(256, 1) void wide_mfma_kernel(AttnParams p, int q_g
 
   // K and V slices in separate arrays: the compiler then only waits for the DMA into the array a
   // read touches, so V of the next block can stay in flight while K is read
-  __shared__ __attribute__((aligned(16))) float lds_k[4 * SLICE];  // [wave][SLICE]
-  __shared__ __attribute__((aligned(16))) float lds_v[4 * SLICE];
-  __shared__ __attribute__((aligned(16))) f32x4 lds_s[4 * 4 * 64];      // [wave][r/4][lane]
+  __shared__ __attribute__((aligned(16))) float lds_k[NW * SLICE];  // [wave][SLICE]
+  __shared__ __attribute__((aligned(16))) float lds_v[NW * SLICE];
+  __shared__ __attribute__((aligned(16))) f32x4 lds_s[NW * 4 * 64];      // [wave][r/4][lane]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -164,12 +165,35 @@ __global__ __launch_bounds__(256, 1) void wide_mfma_kernel(AttnParams p, int q_g
       lds_s[(wave * 4 + k4) * 64 + lane] = x;
     }
     __syncthreads();
+    // Two-stage sum: wave w adds up its 1/NW of the tile over all NW partials (in wave order) and
+    // writes the sum back into partial 0 at the same places, which no other wave reads; after the
+    // barrier every wave reads the summed tile from partial 0.
+    {
+      float* ldsf = reinterpret_cast<float*>(lds_s);
+      constexpr int PER_LANE = 1024 / NW / 64;  // floats of the tile each lane sums
+      const int e0 = wave * (1024 / NW) + lane * PER_LANE;
+      if constexpr (PER_LANE == 4) {
+        f32x4 a = *reinterpret_cast<const f32x4*>(ldsf + e0);
+#pragma unroll
+        for (int ww = 1; ww < NW; ++ww) a += *reinterpret_cast<const f32x4*>(ldsf + ww * 1024 + e0);
+        *reinterpret_cast<f32x4*>(ldsf + e0) = a;
+      } else {
+        static_assert(PER_LANE == 2, "4 or 8 waves");
+        float2 a = *reinterpret_cast<const float2*>(ldsf + e0);
+#pragma unroll
+        for (int ww = 1; ww < NW; ++ww) {
+          const float2 b = *reinterpret_cast<const float2*>(ldsf + ww * 1024 + e0);
+          a.x += b.x;
+          a.y += b.y;
+        }
+        *reinterpret_cast<float2*>(ldsf + e0) = a;
+      }
+    }
+    __syncthreads();
     float u[16];
 #pragma unroll
     for (int k4 = 0; k4 < 4; ++k4) {
-      f32x4 a = lds_s[(0 * 4 + k4) * 64 + lane];
-#pragma unroll
-      for (int ww = 1; ww < 4; ++ww) a += lds_s[(ww * 4 + k4) * 64 + lane];
+      const f32x4 a = lds_s[k4 * 64 + lane];
       u[4 * k4 + 0] = a[0];
       u[4 * k4 + 1] = a[1];
       u[4 * k4 + 2] = a[2];
@@ -186,10 +210,10 @@ __global__ __launch_bounds__(256, 1) void wide_mfma_kernel(AttnParams p, int q_g
     // ---- online softmax with a lazily moved reference
     float mb = u[0];
 #pragma unroll
-    for (int r = 1; r < 16; ++r) mb = fmaxf(mb, u[r]);
+    for (int r = 1; r < 16; ++r) mb = max_nan(mb, u[r]);
     mb = max_with_partner(mb);
     if (__builtin_amdgcn_ballot_w64(mb > m + kRescaleSlack) != 0) {
-      const float m_new = fmaxf(m, mb);
+      const float m_new = max_nan(m, mb);
       const float alpha = fast_exp2(m - m_new);
       m = m_new;
       l *= alpha;
@@ -331,23 +355,29 @@ __global__ __launch_bounds__(256) void wide_merge_kernel(AttnParams p, int q_gro
   *reinterpret_cast<f32x4*>(p.o + p.o_off + (int64_t)b * p.so + (int64_t)qi * p.ldo + h * D + 4 * d4) = y;
 }
 
+// Waves per workgroup: each owns D / NW head dims. D = 512 runs 8 waves (two per SIMD, 160 KiB of
+// LDS), D = 256 runs 4 (80 KiB, two workgroups per CU).
+template <int D>
+constexpr int kWideWaves = D == 512 ? 8 : 4;
+
 template <int D>
 hipError_t launch_d(const AttnParams& p, const WidePlan& plan, float* ws, hipStream_t stream) {
+  constexpr int NW = kWideWaves<D>;
   const int64_t n = (int64_t)p.B * p.H * plan.q_groups * plan.nks;
   if (n > 0x7fffffff) return hipErrorInvalidConfiguration;
-  const dim3 grid((unsigned)n), block(256);
+  const dim3 grid((unsigned)n), block(64 * NW);
   if (p.mask_mode == MASK_KEY_LEN)
-    hipLaunchKernelGGL((wide_mfma_kernel<D, MASK_KEY_LEN>), grid, block, 0, stream, p, plan.q_groups, plan.nks,
+    hipLaunchKernelGGL((wide_mfma_kernel<D, NW, MASK_KEY_LEN>), grid, block, 0, stream, p, plan.q_groups, plan.nks,
                        plan.chunk, ws);
   else
-    hipLaunchKernelGGL((wide_mfma_kernel<D, MASK_NONE>), grid, block, 0, stream, p, plan.q_groups, plan.nks,
+    hipLaunchKernelGGL((wide_mfma_kernel<D, NW, MASK_NONE>), grid, block, 0, stream, p, plan.q_groups, plan.nks,
                        plan.chunk, ws);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || plan.nks == 1) return e;
   const int64_t threads = (int64_t)p.B * p.H * plan.q_groups * 32 * (D / 4);
   const int64_t blocks = (threads + 255) / 256;
   if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((wide_merge_kernel<D>), dim3((unsigned)blocks), block, 0, stream, p, plan.q_groups, plan.nks, ws);
+  hipLaunchKernelGGL((wide_merge_kernel<D>), dim3((unsigned)blocks), dim3(256), 0, stream, p, plan.q_groups, plan.nks, ws);
   return hipGetLastError();
 }
 
