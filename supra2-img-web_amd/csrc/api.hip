@@ -358,7 +358,7 @@ int choose(const sa::AttnParams& p, Choice* c) {
   // The MFMA kernels address a copy's rows (up to 128) as 32-bit byte offsets from the block's
   // first row; longer strides take the generic kernel, whose addresses are 64-bit.
   const bool off32 = p.ldk < ((int64_t)1 << 22) && p.ldv < ((int64_t)1 << 22);
-  if ((p.D == 64 || p.D == 128) && vec && off32) {
+  if ((p.D == 64 || p.D == 128) && vec && off32 && sa::flash_mfma_args_fit(p)) {
     // Units of 32 queries; below ~2 waves per SIMD (256 CUs x 4 SIMDs) split the key blocks
     // across the waves of a workgroup so that more SIMDs get work.
     const int64_t units = (int64_t)p.B * p.H * ((p.Lq + 31) / 32);

@@ -54,6 +54,8 @@
 //   V: chunk c of row r at c ^ (8 * ((r >> 2) & 1)), so the two half-waves (rows 4 apart) read
 //      disjoint bank halves.
 
+#include <string.h>
+
 #include <type_traits>
 
 #include "common.h"
@@ -81,8 +83,39 @@ constexpr int kMinBlocksPerCU = (D == 64 && NSPLIT == 1 && BIAS == BIAS_NONE && 
 // memory system takes to deliver the first tiles of one workgroup per CU over the whole chip.
 constexpr unsigned kStaggerTicks = 350;
 
-template <int D, int NSPLIT, int BIAS, int MASK>
-__global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void flash_mfma_kernel(AttnParams p, int q_tiles, int stagger_cus) {
+// Kernel arguments, packed into 112 bytes: the runtime starts launches with at most 112 bytes of
+// explicit arguments about 0.8 us sooner than larger ones (measured back to back on MI355X), which
+// is a tenth of a small call. Pointers carry the callers' element offsets; strides are 32-bit
+// (calls with larger strides take the generic kernel).
+struct FlashArgs {
+  const float* q;  // q + q_off (likewise k, v, o)
+  const float* k;
+  const float* v;
+  float* o;
+  int32_t sq, sk, sv, so;      // batch strides
+  int32_t ldq, ldk, ldv, ldo;  // row strides
+  int32_t Lq, Lk;
+  int32_t tiles;               // workgroups of the launch (the grid size, for the XCD remap)
+  int16_t H, num_buckets;
+  float scale_log2;
+  int32_t aux;       // start-up stagger period in workgroups (unbiased single-split kernels) | key-mask row stride
+  const void* mask;  // key lengths (int32) | key mask (uint8)
+  const float* bias; // dense bias | relative-position table
+  union {
+    const int32_t* lut;  // relative-position bucket LUT
+    int64_t sbias;       // dense bias batch stride
+  };
+};
+static_assert(sizeof(FlashArgs) == 112, "flash kernel arguments must stay within 112 bytes");
+
+// The longest-first sequence schedule: a second kernel argument of the scheduled variant only.
+struct FlashOrder {
+  uint8_t order[kMaxOrder];
+};
+struct NoOrder {};
+
+template <int D, int NSPLIT, int BIAS, int MASK, typename Order>
+__device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord) {
   constexpr int QG = 4 / NSPLIT;         // query groups (of 32) per workgroup
   constexpr int QT = 32 * QG;            // queries per workgroup
   constexpr int KT = 32 * NSPLIT;        // keys staged per step
@@ -109,25 +142,26 @@ __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void
   const int col = lane & 31;
   const int half = lane >> 5;
 
-  int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int q_tiles = (p.Lq + QT - 1) / QT;
+  int tile = xcd_remap(blockIdx.x, p.tiles);
   const int qtile = tile % q_tiles;
   tile /= q_tiles;
   const int h = tile % p.H;
   int b = tile / p.H;
-  if constexpr (MASK == MASK_KEY_LEN_ORDERED) b = p.order[b];  // the longest-first schedule
+  if constexpr (MASK == MASK_KEY_LEN_ORDERED) b = ord.order[b];  // the longest-first schedule
   const int q0 = qtile * QT;
   const int qi = q0 + qg * 32 + col;
   const bool q_valid = qi < p.Lq;
 
   int kv_len = p.Lk;
-  if constexpr (MASK == MASK_KEY_LEN || MASK == MASK_KEY_LEN_ORDERED) kv_len = min(max(p.key_len[b], 0), p.Lk);
+  if constexpr (MASK == MASK_KEY_LEN || MASK == MASK_KEY_LEN_ORDERED) kv_len = min(max(static_cast<const int32_t*>(p.mask)[b], 0), p.Lk);
   const int nblk = (kv_len + 31) >> 5;
   const int nstep = (nblk + NSPLIT - 1) / NSPLIT;
   constexpr bool use_kmask = MASK == MASK_KEY_MASK;
-  const uint8_t* kmask = use_kmask ? p.key_mask + (int64_t)b * p.smask : nullptr;
+  const uint8_t* kmask = use_kmask ? static_cast<const uint8_t*>(p.mask) + (int64_t)b * p.aux : nullptr;
 
-  const float* kbase = p.k + p.k_off + (int64_t)b * p.sk + h * D;
-  const float* vbase = p.v + p.v_off + (int64_t)b * p.sv + h * D;
+  const float* kbase = p.k + (int64_t)b * p.sk + h * D;
+  const float* vbase = p.v + (int64_t)b * p.sv + h * D;
 
   // ---- HBM -> LDS copy of one step. Lane `lane` of instruction n fills physical chunk
   // (n*4 + wave)*64 + lane of the tile: row `drow[n]`, logical chunk dck[n] (K) / dcv[n] (V).
@@ -201,11 +235,11 @@ __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void
   float m = kMaxSeed;
   float l = 0.f;
 
-  // ---- start-up stagger (stagger_cus > 0 only for the 4-workgroups-per-CU kernels): the g-th
+  // ---- start-up stagger (p.aux > 0 only for the 4-workgroups-per-CU kernels): the g-th
   // workgroup of each CU in the first residency waits g steps before its first loads
   if constexpr (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK> == 4) {
-    if (stagger_cus > 0) {
-      const unsigned gen = blockIdx.x / (unsigned)stagger_cus;
+    if (p.aux > 0) {
+      const unsigned gen = blockIdx.x / (unsigned)p.aux;
       if (gen > 0 && gen < 4) {
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
         while (__builtin_amdgcn_s_memrealtime() - t0 < gen * kStaggerTicks) __builtin_amdgcn_s_sleep(2);
@@ -218,7 +252,7 @@ __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void
   float qr[QREG];
   {
     // unconditional loads from a clamped row (no branch per load); rows past Lq are zeroed after
-    const float* src = p.q + p.q_off + (int64_t)b * p.sq + (int64_t)min(qi, p.Lq - 1) * p.ldq + h * D;
+    const float* src = p.q + (int64_t)b * p.sq + (int64_t)min(qi, p.Lq - 1) * p.ldq + h * D;
     f32x4 xq[QREG / 4];
 #pragma unroll
     for (int i = 0; i < QREG / 4; ++i) xq[i] = *reinterpret_cast<const f32x4*>(src + 4 * (2 * i + half));
@@ -426,7 +460,7 @@ __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void
     }
     constexpr int RPI = 64 / CPR;  // rows per store instruction
     const int rsub = lane / CPR, cidx = lane % CPR;
-    float* obase = p.o + p.o_off + (int64_t)b * p.so + h * D;
+    float* obase = p.o + (int64_t)b * p.so + h * D;
     if ((int64_t)p.Lq * p.ldo < (int64_t)1 << 29) {
       // byte offsets of every row fit in 31 bits: buffer stores from a scalar base
       const __amdgpu_buffer_rsrc_t orsrc = buffer_rsrc(obase);
@@ -449,7 +483,7 @@ __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void
       }
     }
   } else if (q_valid) {
-    float* dst = p.o + p.o_off + (int64_t)b * p.so + (int64_t)qi * p.ldo + h * D + 4 * half;
+    float* dst = p.o + (int64_t)b * p.so + (int64_t)qi * p.ldo + h * D + 4 * half;
 #pragma unroll
     for (int t = 0; t < NDB; ++t) {
 #pragma unroll
@@ -466,21 +500,38 @@ __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void
 }
 
 template <int D, int NSPLIT, int BIAS, int MASK>
-hipError_t launch_one(const AttnParams& p, int q_tiles, dim3 grid, int num_cus, hipStream_t stream) {
+__global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void flash_mfma_kernel(FlashArgs p) {
+  flash_body<D, NSPLIT, BIAS, MASK>(p, NoOrder{});
+}
+
+template <int D, int NSPLIT, int BIAS>
+__global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK_KEY_LEN_ORDERED>)) void flash_mfma_ordered_kernel(
+    FlashArgs p, FlashOrder ord) {
+  flash_body<D, NSPLIT, BIAS, MASK_KEY_LEN_ORDERED>(p, ord);
+}
+
+template <int D, int NSPLIT, int BIAS, int MASK>
+hipError_t launch_one(FlashArgs a, const AttnParams& p, dim3 grid, int num_cus, hipStream_t stream) {
   // stagger only launches with more than one workgroup per CU
-  const int stagger_cus = (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK> == 4 && (int64_t)grid.x > num_cus) ? num_cus : 0;
-  hipLaunchKernelGGL((flash_mfma_kernel<D, NSPLIT, BIAS, MASK>), grid, dim3(256), 0, stream, p, q_tiles, stagger_cus);
+  if constexpr (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK> == 4) a.aux = (int64_t)grid.x > num_cus ? num_cus : 0;
+  if constexpr (MASK == MASK_KEY_LEN_ORDERED) {
+    FlashOrder ord;
+    memcpy(ord.order, p.order, sizeof ord.order);
+    hipLaunchKernelGGL((flash_mfma_ordered_kernel<D, NSPLIT, BIAS>), grid, dim3(256), 0, stream, a, ord);
+  } else {
+    hipLaunchKernelGGL((flash_mfma_kernel<D, NSPLIT, BIAS, MASK>), grid, dim3(256), 0, stream, a);
+  }
   return hipGetLastError();
 }
 
 template <int D, int NSPLIT, int BIAS>
-hipError_t launch_mask(const AttnParams& p, int q_tiles, dim3 grid, int num_cus, hipStream_t stream) {
+hipError_t launch_mask(const FlashArgs& a, const AttnParams& p, dim3 grid, int num_cus, hipStream_t stream) {
   switch (p.mask_mode) {
-    case MASK_NONE: return launch_one<D, NSPLIT, BIAS, MASK_NONE>(p, q_tiles, grid, num_cus, stream);
+    case MASK_NONE: return launch_one<D, NSPLIT, BIAS, MASK_NONE>(a, p, grid, num_cus, stream);
     case MASK_KEY_LEN:
-      if (p.order_n > 0) return launch_one<D, NSPLIT, BIAS, MASK_KEY_LEN_ORDERED>(p, q_tiles, grid, num_cus, stream);
-      return launch_one<D, NSPLIT, BIAS, MASK_KEY_LEN>(p, q_tiles, grid, num_cus, stream);
-    case MASK_KEY_MASK: return launch_one<D, NSPLIT, BIAS, MASK_KEY_MASK>(p, q_tiles, grid, num_cus, stream);
+      if (p.order_n > 0) return launch_one<D, NSPLIT, BIAS, MASK_KEY_LEN_ORDERED>(a, p, grid, num_cus, stream);
+      return launch_one<D, NSPLIT, BIAS, MASK_KEY_LEN>(a, p, grid, num_cus, stream);
+    case MASK_KEY_MASK: return launch_one<D, NSPLIT, BIAS, MASK_KEY_MASK>(a, p, grid, num_cus, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -490,17 +541,55 @@ hipError_t launch_split(const AttnParams& p, int num_cus, hipStream_t stream) {
   constexpr int QT = 32 * (4 / NSPLIT);
   const int q_tiles = (p.Lq + QT - 1) / QT;
   const int64_t n = (int64_t)p.B * p.H * q_tiles;
-  if (n > 0x7fffffff) return hipErrorInvalidConfiguration;
+  if (n > 0x7fffffff || !flash_mfma_args_fit(p)) return hipErrorInvalidConfiguration;
   const dim3 grid((unsigned)n);
+  FlashArgs a;
+  memset(&a, 0, sizeof a);
+  a.q = p.q + p.q_off;
+  a.k = p.k + p.k_off;
+  a.v = p.v + p.v_off;
+  a.o = p.o + p.o_off;
+  a.sq = (int32_t)p.sq;
+  a.sk = (int32_t)p.sk;
+  a.sv = (int32_t)p.sv;
+  a.so = (int32_t)p.so;
+  a.ldq = (int32_t)p.ldq;
+  a.ldk = (int32_t)p.ldk;
+  a.ldv = (int32_t)p.ldv;
+  a.ldo = (int32_t)p.ldo;
+  a.Lq = p.Lq;
+  a.Lk = p.Lk;
+  a.tiles = (int32_t)n;
+  a.H = (int16_t)p.H;
+  a.scale_log2 = p.scale_log2;
+  if (p.mask_mode == MASK_KEY_LEN) a.mask = p.key_len;
+  if (p.mask_mode == MASK_KEY_MASK) {
+    a.mask = p.key_mask;
+    a.aux = (int32_t)p.smask;
+  }
+  a.bias = p.bias;
+  if (p.bias_mode == BIAS_RELPOS) {
+    a.lut = p.lut;
+    a.num_buckets = (int16_t)p.num_buckets;
+  } else {
+    a.sbias = p.sbias;
+  }
   switch (p.bias_mode) {
-    case BIAS_NONE: return launch_mask<D, NSPLIT, BIAS_NONE>(p, q_tiles, grid, num_cus, stream);
-    case BIAS_DENSE: return launch_mask<D, NSPLIT, BIAS_DENSE>(p, q_tiles, grid, num_cus, stream);
-    case BIAS_RELPOS: return launch_mask<D, NSPLIT, BIAS_RELPOS>(p, q_tiles, grid, num_cus, stream);
+    case BIAS_NONE: return launch_mask<D, NSPLIT, BIAS_NONE>(a, p, grid, num_cus, stream);
+    case BIAS_DENSE: return launch_mask<D, NSPLIT, BIAS_DENSE>(a, p, grid, num_cus, stream);
+    case BIAS_RELPOS: return launch_mask<D, NSPLIT, BIAS_RELPOS>(a, p, grid, num_cus, stream);
     default: return hipErrorInvalidValue;
   }
 }
 
 }  // namespace
+
+bool flash_mfma_args_fit(const AttnParams& p) {
+  const int64_t lim = 0x7fffffff;
+  return p.ldq <= lim && p.ldk <= lim && p.ldv <= lim && p.ldo <= lim && p.sq <= lim && p.sk <= lim &&
+         p.sv <= lim && p.so <= lim && p.H <= 0x7fff && (p.mask_mode != MASK_KEY_MASK || p.smask <= lim) &&
+         (p.bias_mode != BIAS_RELPOS || p.num_buckets <= 0x7fff);
+}
 
 const char* flash_mfma_name(int D, int nsplit) {
   if (D == 64) return nsplit == 4 ? "flash_mfma_d64_split4" : nsplit == 2 ? "flash_mfma_d64_split2" : "flash_mfma_d64";

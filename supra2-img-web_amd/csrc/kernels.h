@@ -46,6 +46,9 @@ constexpr int MASK_KEY_LEN_ORDERED = 3;
 // device's CU count) sets the start-up stagger of the single-split kernels.
 hipError_t launch_flash_mfma(const AttnParams& p, int nsplit, int num_cus, hipStream_t stream);
 const char* flash_mfma_name(int D, int nsplit);
+// The flash kernels take 32-bit strides, at most 32767 heads and buckets; other calls take the
+// generic kernel.
+bool flash_mfma_args_fit(const AttnParams& p);
 
 // One compiled flash_mfma_kernel instantiation: <D, nsplit, bias (BIAS_*), mask (MASK_* or
 // MASK_KEY_LEN_ORDERED)>.
