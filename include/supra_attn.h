@@ -151,6 +151,8 @@ const char* sa_attention_kernel_name(const sa_attn_args* args);
 #define SA_KERNEL_FLASH 1   /* flash_mfma_kernel<head_dim, key_split, bias_mode, mask_variant> */
 #define SA_KERNEL_WIDE 2    /* wide_mfma_kernel<head_dim, mask_variant>, + a merge kernel when key_chunks > 1 */
 #define SA_KERNEL_GENERIC 3 /* generic_kernel (any head dim <= 1024, any alignment) */
+#define SA_KERNEL_FLASH_SMALL 4 /* flash_small_kernel<key_split waves, bias_mode, mask_variant>: head dim 64,
+                                   one workgroup per 32 queries, for launches of at most 256 such groups */
 /* mask_variant beyond the SA_MASK_* values: per-sequence key lengths plus the longest-first
  * sequence schedule (SA_MASK_KEY_LEN with key_len_host, 8 <= B <= 256, order not the identity) */
 #define SA_MASK_VARIANT_KEY_LEN_SCHEDULED 3
@@ -159,7 +161,7 @@ typedef struct sa_attn_plan {
   uint32_t struct_size;    /* set to sizeof(sa_attn_plan) before the call */
   int32_t kernel;          /* SA_KERNEL_* */
   int32_t head_dim;        /* head dim the kernel is compiled for (the call's D for GENERIC) */
-  int32_t key_split;       /* FLASH: waves of a workgroup that split one query group's key blocks */
+  int32_t key_split;       /* FLASH, FLASH_SMALL: waves of a workgroup that split one query group's key blocks */
   int32_t key_chunks;      /* WIDE: workgroups that split one query group's keys (merged after) */
   int32_t bias_mode;       /* SA_BIAS_* compiled into the kernel */
   int32_t mask_variant;    /* SA_MASK_* compiled into the kernel, or SA_MASK_VARIANT_KEY_LEN_SCHEDULED */

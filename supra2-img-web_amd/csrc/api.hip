@@ -317,7 +317,7 @@ int64_t align256(int64_t b) { return (b + 255) & ~(int64_t)255; }
 // gives the same kernel choice as the real workspace, which is 16-byte aligned at least).
 int vae_plan(const sa_vae_attn_args* a, char* ws, VaeLayout* L, sa_attn_args* at);
 
-enum class Path { kFlash, kWide, kGeneric };
+enum class Path { kFlash, kSmall, kWide, kGeneric };
 
 struct Choice {
   Path path;
@@ -359,13 +359,20 @@ int choose(const sa::AttnParams& p, Choice* c) {
   // first row; longer strides take the generic kernel, whose addresses are 64-bit.
   const bool off32 = p.ldk < ((int64_t)1 << 22) && p.ldv < ((int64_t)1 << 22);
   if ((p.D == 64 || p.D == 128) && vec && off32 && sa::flash_mfma_args_fit(p)) {
-    // Units of 32 queries; below ~2 waves per SIMD (256 CUs x 4 SIMDs) split the key blocks
-    // across the waves of a workgroup so that more SIMDs get work.
+    // Units of 32 queries. Head dim 64 with at most one unit per CU (the batch-2 DiT calls, a T5
+    // prompt): one workgroup per unit with its key blocks dealt to 4 waves. Otherwise the
+    // 128-query flash kernel, which below ~2 waves per SIMD (256 CUs x 4 SIMDs) splits the key
+    // blocks across two waves of each workgroup.
     const int64_t units = (int64_t)p.B * p.H * ((p.Lq + 31) / 32);
     const int nblk = (p.Lk + 31) / 32;
+    if (p.D == 64 && units <= 256 && nblk >= 2) {
+      c->path = Path::kSmall;
+      c->nsplit = sa::flash_small_waves(p);
+      c->name = sa::flash_small_name(c->nsplit);
+      return SA_OK;
+    }
     int nsplit = 1;
     if (units < 2048 && nblk >= 2) nsplit = 2;
-    if (units < 1024 && nblk >= 4 && p.D == 64) nsplit = 4;
     c->path = Path::kFlash;
     c->nsplit = nsplit;
     c->name = sa::flash_mfma_name(p.D, nsplit);
@@ -429,6 +436,8 @@ int run_attention(const sa_attn_args* args, void* stream, bool own_scratch) {
   hipError_t e;
   if (c.path == Path::kFlash) {
     e = sa::launch_flash_mfma(p, c.nsplit, num_cus(), (hipStream_t)stream);
+  } else if (c.path == Path::kSmall) {
+    e = sa::launch_flash_small(p, (hipStream_t)stream);
   } else if (c.path == Path::kWide) {
     float* ws = nullptr;
     if (c.wide.ws_floats > 0) {
@@ -613,6 +622,12 @@ int sa_attention_plan(const sa_attn_args* args, sa_attn_plan* plan) {
     plan->mask_variant = fv.mask;
     plan->keys_per_step = 32 * fv.nsplit;
     plan->workgroups = sa::flash_mfma_workgroups(p, c.nsplit);
+  } else if (c.path == Path::kSmall) {
+    plan->kernel = SA_KERNEL_FLASH_SMALL;
+    plan->head_dim = p.D;
+    plan->key_split = c.nsplit;
+    plan->keys_per_step = 32 * c.nsplit;
+    plan->workgroups = sa::flash_small_workgroups(p);
   } else if (c.path == Path::kWide) {
     plan->kernel = SA_KERNEL_WIDE;
     plan->head_dim = p.D;
@@ -629,8 +644,9 @@ int sa_attention_plan(const sa_attn_args* args, sa_attn_plan* plan) {
 }
 
 int32_t sa_attention_variant_count(void) {
-  // flash variants, then the wide kernel (D 256, 512 x no mask / key lengths), then generic
-  return sa::flash_mfma_variants(nullptr, 0) + 4 + 1;
+  // flash variants, small-launch variants, the wide kernel (D 256, 512 x no mask / key lengths),
+  // then generic
+  return sa::flash_mfma_variants(nullptr, 0) + sa::flash_small_variants(nullptr, 0) + 4 + 1;
 }
 
 int sa_attention_variant(int32_t index, sa_attn_plan* plan) {
@@ -639,10 +655,24 @@ int sa_attention_variant(int32_t index, sa_attn_plan* plan) {
     return fail(SA_ERR_INVALID, "plan struct_size %u does not match sizeof(sa_attn_plan) = %zu", plan->struct_size,
                 sizeof(sa_attn_plan));
   const int nflash = sa::flash_mfma_variants(nullptr, 0);
+  const int nsmall = sa::flash_small_variants(nullptr, 0);
   if (index < 0 || index >= sa_attention_variant_count())
     return fail(SA_ERR_INVALID, "variant index %d outside [0, %d)", index, sa_attention_variant_count());
   *plan = sa_attn_plan{};
   plan->struct_size = sizeof(sa_attn_plan);
+  if (index >= nflash && index < nflash + nsmall) {
+    sa::FlashVariant v[64];
+    if (sa::flash_small_variants(v, 64) > 64) return fail(SA_ERR_UNSUPPORTED, "variant table overflow");
+    const sa::FlashVariant& x = v[index - nflash];
+    plan->kernel = SA_KERNEL_FLASH_SMALL;
+    plan->head_dim = x.D;
+    plan->key_split = x.nsplit;
+    plan->bias_mode = x.bias;
+    plan->mask_variant = x.mask;
+    plan->name = sa::flash_small_name(x.nsplit);
+    return ok();
+  }
+  if (index >= nflash) index -= nsmall;
   if (index < nflash) {
     sa::FlashVariant v[128];
     static_assert(sizeof(v) / sizeof(v[0]) >= 60, "variant table");

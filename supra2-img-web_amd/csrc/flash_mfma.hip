@@ -83,31 +83,6 @@ constexpr int kMinBlocksPerCU = (D == 64 && NSPLIT == 1 && BIAS == BIAS_NONE && 
 // memory system takes to deliver the first tiles of one workgroup per CU over the whole chip.
 constexpr unsigned kStaggerTicks = 350;
 
-// Kernel arguments, packed into 112 bytes: the runtime starts launches with at most 112 bytes of
-// explicit arguments about 0.8 us sooner than larger ones (measured back to back on MI355X), which
-// is a tenth of a small call. Pointers carry the callers' element offsets; strides are 32-bit
-// (calls with larger strides take the generic kernel).
-struct FlashArgs {
-  const float* q;  // q + q_off (likewise k, v, o)
-  const float* k;
-  const float* v;
-  float* o;
-  int32_t sq, sk, sv, so;      // batch strides
-  int32_t ldq, ldk, ldv, ldo;  // row strides
-  int32_t Lq, Lk;
-  int32_t tiles;               // workgroups of the launch (the grid size, for the XCD remap)
-  int16_t H, num_buckets;
-  float scale_log2;
-  int32_t aux;       // start-up stagger period in workgroups (unbiased single-split kernels) | key-mask row stride
-  const void* mask;  // key lengths (int32) | key mask (uint8)
-  const float* bias; // dense bias | relative-position table
-  union {
-    const int32_t* lut;  // relative-position bucket LUT
-    int64_t sbias;       // dense bias batch stride
-  };
-};
-static_assert(sizeof(FlashArgs) == 112, "flash kernel arguments must stay within 112 bytes");
-
 // The longest-first sequence schedule: a second kernel argument of the scheduled variant only.
 struct FlashOrder {
   uint8_t order[kMaxOrder];
@@ -543,6 +518,18 @@ hipError_t launch_split(const AttnParams& p, int num_cus, hipStream_t stream) {
   const int64_t n = (int64_t)p.B * p.H * q_tiles;
   if (n > 0x7fffffff || !flash_mfma_args_fit(p)) return hipErrorInvalidConfiguration;
   const dim3 grid((unsigned)n);
+  const FlashArgs a = flash_args(p, n);
+  switch (p.bias_mode) {
+    case BIAS_NONE: return launch_mask<D, NSPLIT, BIAS_NONE>(a, p, grid, num_cus, stream);
+    case BIAS_DENSE: return launch_mask<D, NSPLIT, BIAS_DENSE>(a, p, grid, num_cus, stream);
+    case BIAS_RELPOS: return launch_mask<D, NSPLIT, BIAS_RELPOS>(a, p, grid, num_cus, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+FlashArgs flash_args(const AttnParams& p, int64_t tiles) {
   FlashArgs a;
   memset(&a, 0, sizeof a);
   a.q = p.q + p.q_off;
@@ -559,7 +546,7 @@ hipError_t launch_split(const AttnParams& p, int num_cus, hipStream_t stream) {
   a.ldo = (int32_t)p.ldo;
   a.Lq = p.Lq;
   a.Lk = p.Lk;
-  a.tiles = (int32_t)n;
+  a.tiles = (int32_t)tiles;
   a.H = (int16_t)p.H;
   a.scale_log2 = p.scale_log2;
   if (p.mask_mode == MASK_KEY_LEN) a.mask = p.key_len;
@@ -574,15 +561,8 @@ hipError_t launch_split(const AttnParams& p, int num_cus, hipStream_t stream) {
   } else {
     a.sbias = p.sbias;
   }
-  switch (p.bias_mode) {
-    case BIAS_NONE: return launch_mask<D, NSPLIT, BIAS_NONE>(a, p, grid, num_cus, stream);
-    case BIAS_DENSE: return launch_mask<D, NSPLIT, BIAS_DENSE>(a, p, grid, num_cus, stream);
-    case BIAS_RELPOS: return launch_mask<D, NSPLIT, BIAS_RELPOS>(a, p, grid, num_cus, stream);
-    default: return hipErrorInvalidValue;
-  }
+  return a;
 }
-
-}  // namespace
 
 bool flash_mfma_args_fit(const AttnParams& p) {
   const int64_t lim = 0x7fffffff;
@@ -592,18 +572,18 @@ bool flash_mfma_args_fit(const AttnParams& p) {
 }
 
 const char* flash_mfma_name(int D, int nsplit) {
-  if (D == 64) return nsplit == 4 ? "flash_mfma_d64_split4" : nsplit == 2 ? "flash_mfma_d64_split2" : "flash_mfma_d64";
+  if (D == 64) return nsplit == 2 ? "flash_mfma_d64_split2" : "flash_mfma_d64";
   if (D == 128) return nsplit == 2 ? "flash_mfma_d128_split2" : "flash_mfma_d128";
   return nullptr;
 }
 
 // The key splits compiled per head dim: launch_flash_mfma instantiates every (bias, mask) pair for
 // each of them.
-constexpr int kSplits64[] = {1, 2, 4};
+constexpr int kSplits64[] = {1, 2};  // small D = 64 launches take flash_small_kernel instead of a 4-way split
 constexpr int kSplits128[] = {1, 2};
 
 static int compiled_split(int D, int nsplit) {
-  if (D == 64) return nsplit >= 4 ? 4 : nsplit == 2 ? 2 : 1;
+  (void)D;
   return nsplit >= 2 ? 2 : 1;
 }
 
@@ -634,8 +614,7 @@ int flash_mfma_variants(FlashVariant* out, int cap) {
 
 hipError_t launch_flash_mfma(const AttnParams& p, int nsplit, int num_cus, hipStream_t stream) {
   if (p.D == 64) {
-    if (nsplit == 4) return launch_split<64, 4>(p, num_cus, stream);
-    if (nsplit == 2) return launch_split<64, 2>(p, num_cus, stream);
+    if (nsplit >= 2) return launch_split<64, 2>(p, num_cus, stream);
     return launch_split<64, 1>(p, num_cus, stream);
   }
   if (p.D == 128) {

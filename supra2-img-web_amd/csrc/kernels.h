@@ -41,6 +41,33 @@ enum { MASK_NONE = 0, MASK_KEY_LEN = 1, MASK_KEY_MASK = 2 };
 // AttnParams::order, so that the plain key-length variant does not read the schedule at all.
 constexpr int MASK_KEY_LEN_ORDERED = 3;
 
+// Arguments of the flash kernels, packed into 112 bytes: the runtime starts launches with at most
+// 112 bytes of explicit arguments about 0.8 us sooner than larger ones (measured back to back on
+// MI355X), a tenth of a small call. Pointers carry the callers' element offsets; strides are 32-bit
+// (calls with larger strides take the generic kernel).
+struct FlashArgs {
+  const float* q;  // q + q_off (likewise k, v, o)
+  const float* k;
+  const float* v;
+  float* o;
+  int32_t sq, sk, sv, so;      // batch strides
+  int32_t ldq, ldk, ldv, ldo;  // row strides
+  int32_t Lq, Lk;
+  int32_t tiles;               // workgroups of the launch (the grid size, for the XCD remap)
+  int16_t H, num_buckets;
+  float scale_log2;
+  int32_t aux;       // start-up stagger period in workgroups (unbiased single-split kernels) | key-mask row stride
+  const void* mask;  // key lengths (int32) | key mask (uint8)
+  const float* bias; // dense bias | relative-position table
+  union {
+    const int32_t* lut;  // relative-position bucket LUT
+    int64_t sbias;       // dense bias batch stride
+  };
+};
+static_assert(sizeof(FlashArgs) == 112, "flash kernel arguments must stay within 112 bytes");
+// The packed arguments of a call whose launch has `tiles` workgroups (flash_mfma_args_fit(p)).
+FlashArgs flash_args(const AttnParams& p, int64_t tiles);
+
 // Flash kernel on fp32 MFMA for D in {64, 128} with 16-byte aligned rows.
 // nsplit in {1, 2, 4}: key blocks are split across the 4 waves of a workgroup. num_cus (the
 // device's CU count) sets the start-up stagger of the single-split kernels.
@@ -61,6 +88,15 @@ FlashVariant flash_mfma_variant(const AttnParams& p, int nsplit);
 int64_t flash_mfma_workgroups(const AttnParams& p, int nsplit);
 // Every compiled variant, in a fixed order: returns the count and fills out[0, min(count, cap)).
 int flash_mfma_variants(FlashVariant* out, int cap);
+
+// Small launches with head dim 64 (csrc/flash_small.hip): one workgroup per group of 32 queries,
+// its key blocks dealt to 4 waves with K and V in registers; variants <64, 4, bias, mask> with mask
+// in {MASK_NONE, MASK_KEY_LEN, MASK_KEY_MASK} (no sequence schedule).
+int flash_small_waves(const AttnParams& p);
+int64_t flash_small_workgroups(const AttnParams& p);
+const char* flash_small_name(int nw);
+int flash_small_variants(FlashVariant* out, int cap);
+hipError_t launch_flash_small(const AttnParams& p, hipStream_t stream);
 
 // Wide heads (D = 256 or 512, no bias, optional key lengths): head dim split across the waves of
 // a workgroup, keys split across workgroups, partials merged by a second kernel via a workspace.

@@ -97,7 +97,7 @@ def rc_of(args):
 
 
 def test_valid_call_selects_mfma_kernel():
-    assert _lib.kernel_name(good_args()) == "flash_mfma_d64_split4"
+    assert _lib.kernel_name(good_args()) == "flash_small_d64"
     assert _lib.kernel_name(good_args(B=64, o=FAKE + (1 << 36), sq=256 * 1728)) == "flash_mfma_d64"
     assert _lib.kernel_name(good_args(B=16, o=FAKE + (1 << 36))) == "flash_mfma_d64_split2"
     assert _lib.kernel_name(good_args(D=128, H=4, ldo=512, so=256 * 512)) == "flash_mfma_d128_split2"
@@ -106,7 +106,7 @@ def test_valid_call_selects_mfma_kernel():
 def test_generic_kernel_for_row_strides_beyond_32bit_copy_offsets():
     big = 1 << 22  # 128 rows of this stride no longer fit a 31-bit byte offset
     far = FAKE + (1 << 40)  # an output beyond the long k/v extents
-    assert _lib.kernel_name(good_args(ldk=big - 4, ldv=big - 4, sk=256 * big, sv=256 * big, o=far)) == "flash_mfma_d64_split4"
+    assert _lib.kernel_name(good_args(ldk=big - 4, ldv=big - 4, sk=256 * big, sv=256 * big, o=far)) == "flash_small_d64"
     assert _lib.kernel_name(good_args(ldk=big, ldv=1728, sk=256 * big, o=far)) == "generic"
     assert _lib.kernel_name(good_args(ldv=big, sv=256 * big, o=far)) == "generic"
 
@@ -268,7 +268,7 @@ def test_null_args_pointer():
 def test_error_message_clears_on_success():
     lib = _lib.load()
     assert rc_of(good_args(B=0)) == _lib.SA_ERR_INVALID
-    assert _lib.kernel_name(good_args()) == "flash_mfma_d64_split4"
+    assert _lib.kernel_name(good_args()) == "flash_small_d64"
     assert lib.sa_last_error() == b""
 
 

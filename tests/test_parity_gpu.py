@@ -55,7 +55,7 @@ def run_checked(dev, call, *, expect_kernel=None, tol=TOL, check_fp64=True):
 
 def test_dit_self_b2(dev):
     call = workloads.dit_self(B=2, seed=0)
-    run_checked(dev, call, expect_kernel="flash_mfma_d64_split4")
+    run_checked(dev, call, expect_kernel="flash_small_d64")
 
 
 def test_dit_cross_b2(dev):

@@ -117,7 +117,8 @@ def test_draw_reaches_every_kernel():
                              bias=fake + (4 << 34), bucket_lut=fake + (5 << 34), num_buckets=32,
                              mask_mode=call.mask_mode, key_len=fake + (6 << 34), key_mask=fake + (7 << 34), **a)
         names.add(_lib.kernel_name(args).split("_split")[0])
-    assert {"flash_mfma_d64", "flash_mfma_d128", "generic"} <= names and any(n.startswith("wide") for n in names), names
+    assert {"flash_mfma_d64", "flash_mfma_d128", "generic"} <= names, names
+    assert any(n.startswith("wide") for n in names) and any(n.startswith("flash_small") for n in names), names
 
 
 @pytest.mark.parametrize("case", LINEAR, ids=[c["name"] for c in LINEAR])

@@ -6,26 +6,29 @@ from __future__ import annotations
 import pytest
 
 from supra_attn import _lib
-from variant_cases import call_for, fake_args, flash_variants, min_steps_per_wave
+from variant_cases import SMALL, call_for, fake_args, flash_variants, steps_per_wave, variant_id
 
 
 def test_every_compiled_variant_is_enumerated_once():
     vs = _lib.variants()
     flash = flash_variants()
-    assert len(flash) == len(set(flash)) >= 60
+    assert len(flash) == len(set(flash))
+    assert sum(v[0] == _lib.SA_KERNEL_FLASH for v in flash) == 48  # D 64, 128 x splits 1, 2 x 3 biases x 4 masks
+    assert sum(v[0] == SMALL for v in flash) == 9                  # 4 waves x 3 biases x 3 masks
     assert sum(v.kernel == _lib.SA_KERNEL_WIDE for v in vs) == 4
     assert sum(v.kernel == _lib.SA_KERNEL_GENERIC for v in vs) == 1
     assert all(v.name for v in vs)
 
 
-@pytest.mark.parametrize("variant", flash_variants(), ids=lambda v: "d%d_s%d_b%d_m%d" % v)
+@pytest.mark.parametrize("variant", flash_variants(), ids=variant_id)
 def test_case_selects_its_variant(variant):
-    D, split, bias, mask = variant
-    call, host = call_for(D, split, bias, mask)
+    kernel, D, split, bias, mask = variant
+    call, host = call_for(*variant)
     plan = _lib.plan(fake_args(call, host))
-    assert plan.variant() == (_lib.SA_KERNEL_FLASH, D, split, bias, mask), call.name
+    assert plan.variant() == variant, call.name
     assert plan.keys_per_step == 32 * split
-    assert min_steps_per_wave(call, split) >= 2, call.name
+    first, last = steps_per_wave(call, split)
+    assert last >= 2, call.name
     assert call.Lq % 32 != 0 and call.Lk % 32 != 0, "lengths must be ragged"
     assert plan.workgroups > 0 and plan.workspace_bytes == 0
 

@@ -1,4 +1,4 @@
-"""GPU parity of every compiled flash-kernel variant <D, key_split, bias, mask>, each at a shape
+"""GPU parity of every compiled flash and small-launch kernel variant <kernel, D, key_split, bias, mask>, each at a shape
 that real callers give it, with ragged lengths and at least two loop steps per splitting wave,
 against the PyTorch fp32 CPU path and the float64 brute force (both <= 1e-5, relative L2 and
 normwise max). The cases come from variant_cases.py; test_variants.py shows on the host that they
@@ -12,7 +12,7 @@ import pytest
 from oracle import attention as orc
 from supra_attn import _lib
 from supra_attn.runner import Staged
-from variant_cases import call_for, flash_variants
+from variant_cases import call_for, flash_variants, variant_id
 
 pytestmark = pytest.mark.gpu
 
@@ -20,14 +20,13 @@ TOL = 1e-5
 SENTINEL = np.float32(-12345.5)
 
 
-@pytest.mark.parametrize("variant", flash_variants(), ids=lambda v: "d%d_s%d_b%d_m%d" % v)
+@pytest.mark.parametrize("variant", flash_variants(), ids=variant_id)
 def test_variant_parity(dev, variant):
-    D, split, bias, mask = variant
-    call, host = call_for(D, split, bias, mask)
-    print(f"[case] {call.name} B={call.B} H={call.H} D={D} Lq={call.Lq} Lk={call.Lk}", flush=True)
+    call, host = call_for(*variant)
+    print(f"[case] {call.name} B={call.B} H={call.H} D={call.D} Lq={call.Lq} Lk={call.Lk}", flush=True)
     st = Staged(dev, call, out_fill=SENTINEL, host_key_len=host)
     try:
-        assert _lib.plan(st.args).variant() == (_lib.SA_KERNEL_FLASH, D, split, bias, mask)
+        assert _lib.plan(st.args).variant() == variant
         out = st.run()
     finally:
         st.release()

@@ -17,14 +17,15 @@ import numpy as np
 from supra_attn import _lib
 from cases import make_call
 
-# (D, key_split) -> (B, H, Lq, Lk): every B >= 8 (the scheduled key-length variant needs it), and
-# ceil(Lk / 32) >= 2 * key_split (at least two steps for the last splitting wave).
+# (kernel, D, key_split) -> (B, H, Lq, Lk): every B >= 8 (the scheduled key-length variant needs it),
+# and ceil(Lk / 32) >= 2 * key_split: at least two steps (two blocks) for the last splitting wave.
+FLASH, SMALL = _lib.SA_KERNEL_FLASH, _lib.SA_KERNEL_FLASH_SMALL
 SHAPES = {
-    (64, 1): (48, 12, 123, 123),   # T5-like batch of prompts (48 x 12 heads, 4 query tiles of 128)
-    (64, 2): (16, 12, 200, 150),
-    (64, 4): (8, 4, 100, 250),
-    (128, 1): (32, 8, 250, 100),   # head dim 128 (the reference's fused gate admits it, ops.js:112)
-    (128, 2): (8, 2, 100, 150),
+    (FLASH, 64, 1): (48, 12, 123, 123),   # T5-like batch of prompts (48 x 12 heads, 4 query tiles of 128)
+    (FLASH, 64, 2): (16, 12, 200, 150),
+    (FLASH, 128, 1): (32, 8, 250, 100),   # head dim 128 (the reference's fused gate admits it, ops.js:112)
+    (FLASH, 128, 2): (8, 2, 100, 150),
+    (SMALL, 64, 4): (8, 4, 100, 250),     # 128 groups of 32 queries, 8 key blocks: two per wave
 }
 
 MASK_NAMES = {0: "none", 1: "key_len", 2: "key_mask", 3: "key_len_scheduled"}
@@ -42,11 +43,11 @@ def key_lengths(rng, B: int, Lk: int, split: int) -> np.ndarray:
     return kl
 
 
-def call_for(D: int, split: int, bias: int, mask: int, seed: int = 0):
+def call_for(kernel: int, D: int, split: int, bias: int, mask: int, seed: int = 0):
     """(call, host_key_len) for the variant; host_key_len says whether the host copy of the key
     lengths goes with the call (it selects the scheduled variant)."""
-    B, H, Lq, Lk = SHAPES[(D, split)]
-    seed = seed + 1000 * D + 100 * split + 10 * bias + mask
+    B, H, Lq, Lk = SHAPES[(kernel, D, split)]
+    seed = seed + 10000 * kernel + 1000 * D + 100 * split + 10 * bias + mask
     rng = np.random.default_rng(seed)
     mask_mode = {0: _lib.SA_MASK_NONE, 1: _lib.SA_MASK_KEY_LEN, 2: _lib.SA_MASK_KEY_MASK,
                  3: _lib.SA_MASK_KEY_LEN}[mask]
@@ -58,7 +59,7 @@ def call_for(D: int, split: int, bias: int, mask: int, seed: int = 0):
     call = make_call(B=B, H=H, D=D, Lq=Lq, Lk=Lk, seed=seed, scale=scale, packed=(D == 64 and bias == 0),
                      bias_mode=bias, mask_mode=mask_mode, key_len=kl,
                      dense_bias_batched=(bias == _lib.SA_BIAS_DENSE and split == 1),
-                     name=f"flash_d{D}_s{split}_{BIAS_NAMES[bias]}_{MASK_NAMES[mask]}")
+                     name=f"{'small' if kernel == SMALL else 'flash'}_d{D}_s{split}_{BIAS_NAMES[bias]}_{MASK_NAMES[mask]}")
     if mask_mode == _lib.SA_MASK_KEY_MASK:
         call.key_mask[0, :] = 0  # a sequence with no attended key: zeros
     return call, mask == 3
@@ -102,16 +103,21 @@ def fake_args(call, host_key_len: bool) -> _lib.AttnArgs:
 
 
 def flash_variants() -> list[tuple]:
-    """(D, key_split, bias, mask) of every compiled flash variant."""
-    return [(v.head_dim, v.key_split, v.bias_mode, v.mask_variant) for v in _lib.variants()
-            if v.kernel == _lib.SA_KERNEL_FLASH]
+    """(kernel, D, key_split, bias, mask) of every compiled flash and small-launch variant."""
+    return [(v.kernel, v.head_dim, v.key_split, v.bias_mode, v.mask_variant) for v in _lib.variants()
+            if v.kernel in (FLASH, SMALL)]
 
 
-def min_steps_per_wave(call, split: int) -> int:
-    """Loop steps of the busiest splitting wave of the longest sequence (key blocks of 32)."""
+def variant_id(v) -> str:
+    return "%s_d%d_s%d_b%d_m%d" % ((("small" if v[0] == SMALL else "flash"),) + tuple(v[1:]))
+
+
+def steps_per_wave(call, split: int) -> tuple:
+    """Key blocks of the first and of the last splitting wave for the longest sequence (blocks of
+    32 keys dealt round robin)."""
     if call.key_len is not None:
         kv = int(np.clip(call.key_len, 0, call.Lk).max())
     else:
         kv = call.Lk
     nblk = (kv + 31) // 32
-    return (nblk - (split - 1) + split - 1) // split  # blocks of the last splitting wave
+    return (nblk + split - 1) // split, (nblk - (split - 1) + split - 1) // split
