@@ -60,8 +60,8 @@ struct VBlock {
 template <int BIAS, int MASK>
 struct BBlock {
   int bucket;
-  float bv[BIAS == BIAS_DENSE ? 16 : 1];
-  uint8_t km[MASK == MASK_KEY_MASK ? 16 : 1];
+  f32x4 bv[BIAS == BIAS_DENSE ? 4 : 1];       // keys 8g + 4*half + 0..3 in bv[g]
+  uint32_t km[MASK == MASK_KEY_MASK ? 4 : 1];  // their mask bytes, little-endian in km[g]
 };
 
 template <int NW, int BIAS, int MASK>
@@ -102,6 +102,12 @@ __global__ __launch_bounds__(64 * NW, 1) void flash_small_kernel(FlashArgs p) {
   const uint8_t* kmask = MASK == MASK_KEY_MASK ? static_cast<const uint8_t*>(p.mask) + (int64_t)b * p.aux : nullptr;
   const float* brow = nullptr;
   if constexpr (BIAS == BIAS_DENSE) brow = p.bias + (int64_t)b * p.sbias + ((int64_t)h * p.Lq + min(qi, p.Lq - 1)) * p.Lk;
+  // The lane's 16 keys are four runs of 4 (keys k0 + 8g + 4*half + 0..3): one 16-byte dense-bias load
+  // and one 4-byte mask load per run when the rows allow it (whole block inside Lk, aligned rows),
+  // element loads at clamped indices otherwise.
+  const bool bias_vec = BIAS == BIAS_DENSE && ((reinterpret_cast<uintptr_t>(p.bias) | (uintptr_t)p.Lk |
+                                                (uintptr_t)(p.sbias * 4)) & 15) == 0;
+  const bool mask_vec = MASK == MASK_KEY_MASK && (reinterpret_cast<uintptr_t>(kmask) & 3) == 0;
   using BB = BBlock<BIAS, MASK>;
   auto load_b = [&](BB& bb, int j) {
     const int k0 = j * 32;
@@ -110,12 +116,27 @@ __global__ __launch_bounds__(64 * NW, 1) void flash_small_kernel(FlashArgs p) {
       bb.bucket = (lane < 63 && li >= 0 && li <= p.Lq + p.Lk - 2) ? p.lut[li] : -1;
     }
     if constexpr (BIAS == BIAS_DENSE) {
+      if (bias_vec && k0 + 32 <= p.Lk) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) bb.bv[r] = brow[min(k0 + 8 * (r >> 2) + 4 * half + (r & 3), p.Lk - 1)];
+        for (int gq = 0; gq < 4; ++gq) bb.bv[gq] = *reinterpret_cast<const f32x4*>(brow + k0 + 8 * gq + 4 * half);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) bb.bv[r >> 2][r & 3] = brow[min(k0 + 8 * (r >> 2) + 4 * half + (r & 3), p.Lk - 1)];
+      }
     }
     if constexpr (MASK == MASK_KEY_MASK) {
+      if (mask_vec && k0 + 32 <= p.Lk) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) bb.km[r] = kmask[min(k0 + 8 * (r >> 2) + 4 * half + (r & 3), p.Lk - 1)];
+        for (int gq = 0; gq < 4; ++gq) bb.km[gq] = *reinterpret_cast<const uint32_t*>(kmask + k0 + 8 * gq + 4 * half);
+      } else {
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          uint32_t w = 0;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w |= (uint32_t)kmask[min(k0 + 8 * gq + 4 * half + e, p.Lk - 1)] << (8 * e);
+          bb.km[gq] = w;
+        }
+      }
     }
   };
 
@@ -162,7 +183,7 @@ __global__ __launch_bounds__(64 * NW, 1) void flash_small_kernel(FlashArgs p) {
     // fetched before the score MFMAs so that they cover its latency
     float rb = 0.f;
     if constexpr (BIAS == BIAS_RELPOS) {
-      if (bb.bucket >= 0) rb = p.bias[min(bb.bucket, p.num_buckets - 1) * p.H + h] * kLog2e;
+      if (bb.bucket >= 0) rb = p.bias[min(bb.bucket, p.num_buckets - 1) * p.H + h];
     }
     f32x16 s = zero16();
 #pragma unroll
@@ -172,6 +193,8 @@ __global__ __launch_bounds__(64 * NW, 1) void flash_small_kernel(FlashArgs p) {
       s = __builtin_amdgcn_mfma_f32_32x32x2f32(kb.kr[i][2], qr[4 * i + 2], s, 0, 0, 0);
       s = __builtin_amdgcn_mfma_f32_32x32x2f32(kb.kr[i][3], qr[4 * i + 3], s, 0, 0, 0);
     }
+    // keep the permutes of the table value after the MFMAs, which then cover the table load
+    if constexpr (BIAS == BIAS_RELPOS) __builtin_amdgcn_sched_barrier(0);
     float u[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) u[r] = s[r];
@@ -179,17 +202,18 @@ __global__ __launch_bounds__(64 * NW, 1) void flash_small_kernel(FlashArgs p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int e = 31 + 8 * (r >> 2) + 4 * half + (r & 3) - col;  // 0..62
-        u[r] += __int_as_float(__builtin_amdgcn_ds_bpermute(e << 2, __float_as_int(rb)));
+        u[r] = fmaf(__int_as_float(__builtin_amdgcn_ds_bpermute(e << 2, __float_as_int(rb))), kLog2e, u[r]);
       }
     } else if constexpr (BIAS == BIAS_DENSE) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) u[r] = fmaf(bb.bv[r], kLog2e, u[r]);
+      for (int r = 0; r < 16; ++r) u[r] = fmaf(bb.bv[r >> 2][r & 3], kLog2e, u[r]);
     }
     if constexpr (MASK == MASK_KEY_MASK) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = k0 + 8 * (r >> 2) + 4 * half + (r & 3);
-        u[r] = (key < p.Lk && bb.km[r] != 0) ? u[r] : -INFINITY;
+        const uint32_t byte = (bb.km[r >> 2] >> (8 * (r & 3))) & 0xffu;
+        u[r] = (key < p.Lk && byte != 0) ? u[r] : -INFINITY;
       }
     } else if (k0 + 32 > kv_len) {
 #pragma unroll
