@@ -32,13 +32,19 @@
 // Rows past M (x) or N (W) re-read the last row (finite data, never stored); the k-tile holding K
 // clamps its column to K - 8 and only its valid groups of 8 are multiplied (K % 8 == 0).
 //
-// Consecutive tiles along N share the x row block: the tile order (x row block major, remapped so
-// that consecutive tiles run on one XCD) keeps that block in the XCD's L2 while its N tiles run.
+// Tile order (TileOrder): consecutive tiles run on one XCD (xcd_remap), and the tiles are cut into
+// row super-blocks of about one XCD's share of the x row blocks. Inside a super-block the N tiles go
+// in groups of W panels small enough to stay in the XCD's 4 MB L2 (the host sizes the groups), and
+// inside a group the row blocks go in turn, each with the group's panels. A row block's x rows are
+// then read once per group, while they are hot, and a panel once per super-block, instead of all
+// of W cycling through the L2 once per row block.
 
+#include <algorithm>
 #include <type_traits>
 
 #include "common.h"
 #include "kernels.h"
+
 
 namespace sa {
 
@@ -71,10 +77,29 @@ __device__ __forceinline__ float apply_act(float v) {
   return v;
 }
 
+// Row block and N tile of logical tile t: super-blocks of sb_rows row blocks (the last may be
+// shorter), inside one the N tiles in groups of group_n (the last may be narrower), inside a group
+// the row blocks, each with the group's N tiles. Bijective on [0, tiles_m * tiles_n).
+struct TileOrder {
+  int tiles_m, tiles_n, group_n, sb_rows;
+};
+
+__device__ __forceinline__ void tile_coords(int t, const TileOrder& o, int& mi, int& ni) {
+  const int sb_tiles = o.sb_rows * o.tiles_n;
+  const int sb = t / sb_tiles;
+  const int rem = t - sb * sb_tiles;
+  const int rows = min(o.sb_rows, o.tiles_m - sb * o.sb_rows);
+  const int g = rem / (rows * o.group_n);
+  const int off = rem - g * rows * o.group_n;
+  const int w = min(o.group_n, o.tiles_n - g * o.group_n);
+  mi = sb * o.sb_rows + off / w;
+  ni = g * o.group_n + off % w;
+}
+
 // WM x WN accumulators per wave, BK k per tile (16 or 32), NS tiles in flight (LDS stages); the
 // activation and the epilogue are compile-time, so the store loop has no per-element branches.
 template <int WM, int WN, int BK, int NS, int ACT, int EPI>
-__global__ __launch_bounds__(256, 2) void linear_mfma_kernel(LinearParams p, int tiles_n) {
+__global__ __launch_bounds__(256, 2) void linear_mfma_kernel(LinearParams p, TileOrder order) {
   constexpr int BM = 64 * WM;
   constexpr int BN = 64 * WN;
   constexpr int CPR = BK / 4;            // 16-byte chunks per tile row
@@ -100,9 +125,10 @@ __global__ __launch_bounds__(256, 2) void linear_mfma_kernel(LinearParams p, int
   const int col = lane & 31;
   const int half = lane >> 5;
 
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
-  const int m0 = (tile / tiles_n) * BM;
-  const int n0 = (tile % tiles_n) * BN;
+  int mi, ni;
+  tile_coords(xcd_remap(blockIdx.x, order.tiles_m * order.tiles_n), order, mi, ni);
+  const int m0 = mi * BM;
+  const int n0 = ni * BN;
 
   const float* xbase = p.x + p.x_off + (int64_t)m0 * p.ldx;
   const float* wbase = p.w + (int64_t)n0 * p.ldw;
@@ -265,6 +291,10 @@ __global__ __launch_bounds__(256, 2) void linear_mfma_kernel(LinearParams p, int
   const float* rsrc_base = (p.resid ? p.resid : p.y) + p.y_off + (int64_t)mw * p.ldy + nw;  // residual rows
   const __amdgpu_buffer_rsrc_t rr_ = buffer_rsrc(rsrc_base);
   const int ldy4 = 4 * (int)p.ldy;
+  // Plain stores are non-temporal (cache policy NT): y is not read back here, and keeping it out of
+  // the L2 leaves the W panels and x rows there (measured on the 16384-row qkv layer: 1.55x fewer L2
+  // fetches). The residual epilogues keep the default policy: there NT cost 3.5% (proj, cproj).
+  constexpr int kStoreCpol = EPI == LIN_EPI_STORE ? 2 : 0;
   auto store = [&](auto check) {
     constexpr bool kCheck = decltype(check)::value;
 #pragma unroll
@@ -294,7 +324,7 @@ __global__ __launch_bounds__(256, 2) void linear_mfma_kernel(LinearParams p, int
           if (!kCheck || (n_ok && mw + 32 * i + 4 * half + rr < p.M)) {
             float v = apply_act<ACT>(fmaf(acc[i][j][r], p.alpha, bias_n));
             if constexpr (EPI != LIN_EPI_STORE) v = fmaf(gate_n, v, old[r]);
-            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), yr, voff, rr * ldy4, 0);
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), yr, voff, rr * ldy4, kStoreCpol);
           }
         }
       }
@@ -341,13 +371,39 @@ __global__ __launch_bounds__(256) void linear_generic_kernel(LinearParams p) {
   }
 }
 
+// Groups of W panels of at most 2 MB (half an XCD's L2: the other half holds the x rows in flight),
+// as few and as even as possible, over super-blocks of one XCD's share of the row blocks. Grouping
+// reads each x row block once per group; it is used when those extra reads come to at most twice
+// W, which the plain order fetches several times per XCD once W outgrows the L2. Measured FETCH_SIZE
+// at 16384 rows: qkv (W 4 MB, x 4.7 MB per XCD, 2 groups) 150 -> 54 MiB with the NT stores, fc1
+// (W 5.3 MB, 3 groups) 144 -> 83 MiB; fc2 (W 5.3 MB but x 19 MB per XCD) went up 156 -> 199-256 MiB
+// when grouped and keeps the plain order. Timings were unchanged (the layers are MFMA-bound).
+TileOrder tile_order(const LinearParams& p, int bm, int bn) {
+  constexpr int64_t kGroupBytes = 2 << 20;
+  TileOrder o;
+  o.tiles_m = (int)((p.M + bm - 1) / bm);
+  o.tiles_n = (int)((p.N + bn - 1) / bn);
+  o.sb_rows = (o.tiles_m + 7) / 8;
+  o.group_n = o.tiles_n;
+  const int64_t panel = (int64_t)bn * p.K * 4;
+  const int64_t w_bytes = o.tiles_n * panel;
+  const int64_t groups = std::min<int64_t>((w_bytes + kGroupBytes - 1) / kGroupBytes, o.tiles_n);
+  if (groups > 1) {
+    const int group_n = (int)((o.tiles_n + groups - 1) / groups);
+    const int64_t x_share = (int64_t)o.sb_rows * bm * p.K * 4;
+    const int64_t n_groups = (o.tiles_n + group_n - 1) / group_n;
+    if (group_n >= 2 && (n_groups - 1) * x_share <= 2 * w_bytes) o.group_n = group_n;
+  }
+  return o;
+}
+
 template <int WM, int WN, int BK, int NS, int ACT, int EPI>
 hipError_t launch_tiles(const LinearParams& p, hipStream_t stream) {
   const int64_t tm = (p.M + 64 * WM - 1) / (64 * WM);
   const int64_t tn = (p.N + 64 * WN - 1) / (64 * WN);
   if (tm * tn > 0x7fffffff) return hipErrorInvalidConfiguration;
   hipLaunchKernelGGL((linear_mfma_kernel<WM, WN, BK, NS, ACT, EPI>), dim3((unsigned)(tm * tn)), dim3(256), 0, stream, p,
-                     (int)tn);
+                     tile_order(p, 64 * WM, 64 * WN));
   return hipGetLastError();
 }
 
