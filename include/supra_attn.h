@@ -169,6 +169,14 @@ typedef struct sa_attn_plan {
   int64_t workgroups;      /* grid of the attention kernel */
   int64_t workspace_bytes; /* sa_attention_workspace_bytes(args) */
   const char* name;        /* sa_attention_kernel_name(args) (static storage) */
+  /* FLASH launches of more units (query tiles) than fit the GPU at once whose last round holds
+   * few units (at most one small-launch workgroup per CU for them): those last units run in a
+   * second launch of the small-launch kernel, split by keys over tail_key_split waves per 32
+   * queries. tail_kernel is SA_KERNEL_FLASH_SMALL then (0 when there is no second launch),
+   * tail_workgroups its grid. */
+  int32_t tail_kernel;
+  int32_t tail_key_split;
+  int64_t tail_workgroups;
 } sa_attn_plan;
 
 /* Fills *plan for these arguments: SA_OK, or the status sa_attention_f32 would return for a

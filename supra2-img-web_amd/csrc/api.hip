@@ -621,7 +621,14 @@ int sa_attention_plan(const sa_attn_args* args, sa_attn_plan* plan) {
     plan->key_split = fv.nsplit;
     plan->mask_variant = fv.mask;
     plan->keys_per_step = 32 * fv.nsplit;
-    plan->workgroups = sa::flash_mfma_workgroups(p, c.nsplit);
+    plan->workgroups = sa::flash_mfma_workgroups(p, c.nsplit, num_cus());
+    const int64_t tail = sa::flash_mfma_tail_units(p, c.nsplit, num_cus());
+    if (tail > 0) {
+      plan->tail_kernel = SA_KERNEL_FLASH_SMALL;
+      plan->tail_key_split = sa::flash_small_waves(p);
+      int64_t first = 0;
+      plan->tail_workgroups = sa::flash_mfma_tail_groups(p, c.nsplit, num_cus(), &first);
+    }
   } else if (c.path == Path::kSmall) {
     plan->kernel = SA_KERNEL_FLASH_SMALL;
     plan->head_dim = p.D;

@@ -517,14 +517,21 @@ hipError_t launch_split(const AttnParams& p, int num_cus, hipStream_t stream) {
   const int q_tiles = (p.Lq + QT - 1) / QT;
   const int64_t n = (int64_t)p.B * p.H * q_tiles;
   if (n > 0x7fffffff || !flash_mfma_args_fit(p)) return hipErrorInvalidConfiguration;
-  const dim3 grid((unsigned)n);
-  const FlashArgs a = flash_args(p, n);
+  // the last units may go to the small-launch kernel: this launch covers units [0, n - tail)
+  const int64_t tail = flash_mfma_tail_units(p, NSPLIT, num_cus);
+  const dim3 grid((unsigned)(n - tail));
+  const FlashArgs a = flash_args(p, n - tail);
+  hipError_t e;
   switch (p.bias_mode) {
-    case BIAS_NONE: return launch_mask<D, NSPLIT, BIAS_NONE>(a, p, grid, num_cus, stream);
-    case BIAS_DENSE: return launch_mask<D, NSPLIT, BIAS_DENSE>(a, p, grid, num_cus, stream);
-    case BIAS_RELPOS: return launch_mask<D, NSPLIT, BIAS_RELPOS>(a, p, grid, num_cus, stream);
+    case BIAS_NONE: e = launch_mask<D, NSPLIT, BIAS_NONE>(a, p, grid, num_cus, stream); break;
+    case BIAS_DENSE: e = launch_mask<D, NSPLIT, BIAS_DENSE>(a, p, grid, num_cus, stream); break;
+    case BIAS_RELPOS: e = launch_mask<D, NSPLIT, BIAS_RELPOS>(a, p, grid, num_cus, stream); break;
     default: return hipErrorInvalidValue;
   }
+  if (e != hipSuccess || tail == 0) return e;
+  int64_t first = 0;
+  const int64_t count = flash_mfma_tail_groups(p, NSPLIT, num_cus, &first);
+  return launch_flash_small_groups(p, first, count, stream);
 }
 
 }  // namespace
@@ -593,9 +600,39 @@ FlashVariant flash_mfma_variant(const AttnParams& p, int nsplit) {
   return {p.D, compiled_split(p.D, nsplit), p.bias_mode, mask};
 }
 
-int64_t flash_mfma_workgroups(const AttnParams& p, int nsplit) {
+// The 4-per-CU kernels run a launch of more units than that in rounds. Units past the last whole
+// round start only as the first workgroups finish and then run at one wave per SIMD: the batch-56
+// DiT self-attention call (1008 units of 128 queries) took 69.5 us, the batch-57 one (1026 units)
+// 83.9 us. When the units left over fit flash_small at one workgroup (4 waves, 32 queries each) per
+// CU, they go there instead, in a second launch right after this one: batch 57 then took 78.9 us,
+// batch 60 (56 units left) 79.2 us instead of 85.0. Batch 64 (128 left, two such workgroups per
+// CU) took 86.2 us instead of 84.8 and keeps the single launch.
+int64_t flash_mfma_tail_units(const AttnParams& p, int nsplit, int num_cus) {
+  const bool eligible = p.D == 64 && compiled_split(p.D, nsplit) == 1 && p.bias_mode == BIAS_NONE &&
+                        (p.mask_mode == MASK_NONE || (p.mask_mode == MASK_KEY_LEN && p.order_n == 0)) && p.Lk > 32;
+  if (!eligible) return 0;
+  const int64_t tiles = (int64_t)p.B * p.H * ((p.Lq + 127) / 128);
+  const int64_t slots = 4 * (int64_t)num_cus;
+  if (tiles <= slots) return 0;
+  const int64_t rest = tiles % slots;
+  return 4 * rest <= num_cus ? rest : 0;
+}
+
+int64_t flash_mfma_tail_groups(const AttnParams& p, int nsplit, int num_cus, int64_t* first) {
+  const int64_t tail = flash_mfma_tail_units(p, nsplit, num_cus);
+  *first = 0;
+  if (tail == 0) return 0;
+  // unit t = (b*H + h)*q_tiles + qtile holds the 32-query groups from (b*H + h)*q_groups + 4*qtile
+  // on, and the units after it the groups after those
+  const int64_t q_tiles = (p.Lq + 127) / 128, q_groups = (p.Lq + 31) / 32;
+  const int64_t t = (int64_t)p.B * p.H * q_tiles - tail;
+  *first = (t / q_tiles) * q_groups + 4 * (t % q_tiles);
+  return (int64_t)p.B * p.H * q_groups - *first;
+}
+
+int64_t flash_mfma_workgroups(const AttnParams& p, int nsplit, int num_cus) {
   const int qt = 32 * (4 / compiled_split(p.D, nsplit));
-  return (int64_t)p.B * p.H * ((p.Lq + qt - 1) / qt);
+  return (int64_t)p.B * p.H * ((p.Lq + qt - 1) / qt) - flash_mfma_tail_units(p, nsplit, num_cus);
 }
 
 int flash_mfma_variants(FlashVariant* out, int cap) {

@@ -73,7 +73,8 @@ __global__ __launch_bounds__(64 * NW, 1) void flash_small_kernel(FlashArgs p) {
   const int half = lane >> 5;
 
   const int q_groups = (p.Lq + 31) >> 5;
-  int tile = xcd_remap(blockIdx.x, p.tiles);
+  // aux: the key-mask row stride with a key mask, else the first 32-query group of the launch
+  int tile = xcd_remap(blockIdx.x, p.tiles) + (MASK == MASK_KEY_MASK ? 0 : p.aux);
   const int g = tile % q_groups;
   tile /= q_groups;
   const int h = tile % p.H;
@@ -341,10 +342,11 @@ hipError_t launch_mask(const FlashArgs& a, int mask_mode, dim3 grid, hipStream_t
 }
 
 template <int NW>
-hipError_t launch_nw(const AttnParams& p, hipStream_t stream) {
-  const int64_t n = flash_small_workgroups(p);
-  if (n > 0x7fffffff || !flash_mfma_args_fit(p)) return hipErrorInvalidConfiguration;
-  const FlashArgs a = flash_args(p, n);
+hipError_t launch_nw(const AttnParams& p, int64_t first, int64_t n, hipStream_t stream) {
+  if (first + n > 0x7fffffff || !flash_mfma_args_fit(p)) return hipErrorInvalidConfiguration;
+  if (first > 0 && p.mask_mode == MASK_KEY_MASK) return hipErrorInvalidValue;  // aux holds the mask stride
+  FlashArgs a = flash_args(p, n);
+  if (p.mask_mode != MASK_KEY_MASK) a.aux = (int32_t)first;
   const dim3 grid((unsigned)n);
   switch (p.bias_mode) {
     case BIAS_NONE: return launch_mask<NW, BIAS_NONE>(a, p.mask_mode, grid, stream);
@@ -377,7 +379,12 @@ int flash_small_variants(FlashVariant* out, int cap) {
 
 hipError_t launch_flash_small(const AttnParams& p, hipStream_t stream) {
   if (p.D != kD) return hipErrorInvalidValue;
-  return launch_nw<kWaves>(p, stream);
+  return launch_nw<kWaves>(p, 0, flash_small_workgroups(p), stream);
+}
+
+hipError_t launch_flash_small_groups(const AttnParams& p, int64_t first, int64_t count, hipStream_t stream) {
+  if (p.D != kD || first < 0 || count <= 0 || first + count > flash_small_workgroups(p)) return hipErrorInvalidValue;
+  return launch_nw<kWaves>(p, first, count, stream);
 }
 
 }  // namespace sa

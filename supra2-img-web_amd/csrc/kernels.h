@@ -85,7 +85,13 @@ struct FlashVariant {
 // The variant a call launches with this key split.
 FlashVariant flash_mfma_variant(const AttnParams& p, int nsplit);
 // Workgroups of that launch.
-int64_t flash_mfma_workgroups(const AttnParams& p, int nsplit);
+int64_t flash_mfma_workgroups(const AttnParams& p, int nsplit, int num_cus);
+// Units (query tiles) of a flash launch that go to a second, flash_small launch (0 = none), and
+// the 32-query groups [*first, *first + count) they hold (returns count).
+int64_t flash_mfma_tail_units(const AttnParams& p, int nsplit, int num_cus);
+int64_t flash_mfma_tail_groups(const AttnParams& p, int nsplit, int num_cus, int64_t* first);
+// 32-query groups [first, first + count) of the call through flash_small_kernel (no key mask).
+hipError_t launch_flash_small_groups(const AttnParams& p, int64_t first, int64_t count, hipStream_t stream);
 // Every compiled variant, in a fixed order: returns the count and fills out[0, min(count, cap)).
 int flash_mfma_variants(FlashVariant* out, int cap);
 

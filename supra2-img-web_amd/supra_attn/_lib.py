@@ -178,6 +178,9 @@ class AttnPlan(ctypes.Structure):
         ("workgroups", c_int64),
         ("workspace_bytes", c_int64),
         ("name", c_char_p),
+        ("tail_kernel", c_int32),
+        ("tail_key_split", c_int32),
+        ("tail_workgroups", c_int64),
     ]
 
     def __init__(self):

@@ -103,6 +103,42 @@ def test_valid_call_selects_mfma_kernel():
     assert _lib.kernel_name(good_args(D=128, H=4, ldo=512, so=256 * 512)) == "flash_mfma_d128_split2"
 
 
+def big(B, Lq=256, **over):
+    return good_args(B=B, Lq=Lq, sq=Lq * 1728, so=Lq * 576, o=FAKE + (1 << 36), **over)
+
+
+@pytest.mark.parametrize("B,Lq,tail_units,tail_groups", [
+    (56, 256, 0, 0),      # 1008 units: one round on 256 CUs
+    (57, 256, 2, 8),      # 1026: a round of 1024 and two left
+    (60, 256, 56, 224),   # 1080: 56 left, 224 groups of 32 queries
+    (61, 256, 0, 0),      # 1098: 74 left would need 296 small workgroups: one launch
+    (64, 256, 0, 0),      # the batch-64 DiT call: 128 left, one launch
+    (114, 256, 4, 16),    # 2052: two whole rounds and four left
+    (57, 200, 2, 7),      # 7 groups of 32 per head: the tail is one whole head of 2 units
+])
+def test_plan_reports_the_tail_launch(B, Lq, tail_units, tail_groups):
+    """The batch-B, 9-head self-attention call on 256 CUs (the count without a device): the units past
+    the last whole round of 1024 go to flash_small when they fit it at one workgroup per CU."""
+    plan = _lib.plan(big(B, Lq))
+    assert plan.kernel == _lib.SA_KERNEL_FLASH and plan.name == b"flash_mfma_d64"
+    assert plan.workgroups == B * 9 * ((Lq + 127) // 128) - tail_units
+    if tail_units:
+        assert (plan.tail_kernel, plan.tail_key_split, plan.tail_workgroups) == (_lib.SA_KERNEL_FLASH_SMALL, 4,
+                                                                                  tail_groups)
+    else:
+        assert (plan.tail_kernel, plan.tail_workgroups) == (0, 0)
+
+
+@pytest.mark.parametrize("over", [
+    dict(bias_mode=1, bias=FAKE + (3 << 36)),                 # a dense bias
+    dict(mask_mode=2, key_mask=FAKE + (3 << 36), smask=256),  # a key mask
+    dict(Lk=32, sk=32 * 1728, sv=32 * 1728),                  # one key block
+])
+def test_no_tail_launch_outside_the_plain_variants(over):
+    plan = _lib.plan(big(60, **over))
+    assert plan.kernel == _lib.SA_KERNEL_FLASH and plan.tail_kernel == 0
+
+
 def test_generic_kernel_for_row_strides_beyond_32bit_copy_offsets():
     big = 1 << 22  # 128 rows of this stride no longer fit a 31-bit byte offset
     far = FAKE + (1 << 40)  # an output beyond the long k/v extents

@@ -1,0 +1,72 @@
+"""GPU parity of flash launches whose last round goes to the small-launch kernel: more units
+(128-query tiles) than the 4-per-CU kernel holds at once, with few enough left over for one
+small-launch workgroup per CU.
+The first launch covers the leading units, flash_small the 32-query groups of the rest; every
+output row is checked against the PyTorch fp32 CPU path and the float64 brute force (1e-5)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from cases import make_call
+from oracle import attention as orc
+from supra_attn import _lib
+from supra_attn.runner import Staged
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+SENTINEL = np.float32(-12345.5)
+
+
+def tail_units(call) -> int:
+    cus = 256  # MI355X
+    tiles = call.B * call.H * ((call.Lq + 127) // 128)
+    rest = tiles % (4 * cus)
+    return rest if tiles > 4 * cus and 4 * rest <= cus else 0
+
+
+@pytest.mark.parametrize("B,Lq,Lk,mask", [
+    (57, 256, 256, "none"),      # 1026 units: a tail of two
+    (60, 256, 256, "none"),      # 1080 units: a tail of 56 (224 small workgroups)
+    (60, 250, 250, "none"),      # ragged
+    (57, 200, 230, "none"),      # 7 groups of 32 per (b, h): the tail starts inside a head
+    (60, 256, 256, "key_len"),   # per-sequence key lengths (launch order, no host copy)
+])
+def test_tail_launch_parity(dev, B, Lq, Lk, mask):
+    kl = None
+    mode = _lib.SA_MASK_NONE
+    if mask == "key_len":
+        rng = np.random.default_rng(B + Lq)
+        kl = rng.integers(33, Lk + 1, size=B).astype(np.int32)
+        kl[-1] = 0   # a sequence in the tail with no keys: zeros
+        kl[-2] = 40  # and a short one
+        mode = _lib.SA_MASK_KEY_LEN
+    call = make_call(B=B, H=9, D=64, Lq=Lq, Lk=Lk, seed=B * 7 + Lq, packed=(Lq == Lk), mask_mode=mode, key_len=kl,
+                     name=f"tail_B{B}_q{Lq}_k{Lk}_{mask}")
+    print(f"[case] {call.name}", flush=True)
+    st = Staged(dev, call, out_fill=SENTINEL, host_key_len=False)
+    try:
+        plan = _lib.plan(st.args)
+        assert plan.kernel == _lib.SA_KERNEL_FLASH
+        n_tail = tail_units(call)
+        assert n_tail > 0
+        assert plan.workgroups == B * 9 * ((Lq + 127) // 128) - n_tail
+        assert plan.tail_kernel == _lib.SA_KERNEL_FLASH_SMALL and plan.tail_key_split == 4
+        out = st.run()
+    finally:
+        st.release()
+    got = orc.output_view(out, call)
+    e = orc.errors(got, orc.reference_torch(call))
+    assert e["finite"] and e["rel_l2"] <= TOL and e["max_rel"] <= TOL, f"{call.name} vs torch fp32: {e}"
+    e64 = orc.errors(got, orc.reference_fp64(call))
+    assert e64["rel_l2"] <= TOL and e64["max_rel"] <= TOL, f"{call.name} vs fp64: {e64}"
+    if kl is not None:
+        assert (got[kl == 0] == 0).all()
+    ldo = call.args.get("ldo", 0) or call.H * call.D
+    written = np.zeros(out.size, dtype=bool)
+    idx = orc.heads(np.arange(out.size), B=call.B, L=call.Lq, H=call.H, D=call.D, off=call.args.get("o_off", 0),
+                    ld=ldo, sb=call.args.get("so", 0))
+    written[idx.reshape(-1)] = True
+    assert (out.reshape(-1)[~written] == SENTINEL).all()
