@@ -108,6 +108,12 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
   __shared__ float lds_rb[BIAS == BIAS_RELPOS ? 2 * RB : 1];         // [stage][relative bias]
   __shared__ float lds_km[MASK == MASK_KEY_MASK ? 2 * KT : 1];       // [stage][0 or -inf per key]
 
+  // Scheduled key-length launches (workgroups of 1-4 key blocks, a new workgroup starting whenever one
+  // ends) raise the wave priority until their first loads are issued: the schedule lookup, key
+  // length and address arithmetic otherwise wait behind the resident waves' MFMAs (sweep
+  // cross-attention 39.6 -> 38.7 us; raised only after the unit decode it measured 40.6 us, and the
+  // same boost on the self-attention launches cost them about 1 us)
+  if constexpr (MASK == MASK_KEY_LEN_ORDERED) __builtin_amdgcn_s_setprio(3);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   // wave-uniform in a scalar register, so per-block conditions compile to scalar branches
@@ -235,6 +241,7 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
     // rather than after the first barrier (which left the two-step loops of the key-split
     // kernels waiting for their second tile).
     if (nstep > 1) issue(1, 1);
+    if constexpr (MASK == MASK_KEY_LEN_ORDERED) __builtin_amdgcn_s_setprio(0);
 #pragma unroll
     for (int i = 0; i < QREG / 4; ++i) {
       const float sc = q_valid ? p.scale_log2 : 0.f;
