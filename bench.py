@@ -20,6 +20,14 @@ The same JSON line carries:
 config) `--launches` times, then copies a 256 MiB device buffer 4 times with the runtime's copy
 kernel: a short program for rocprofv3 counter passes, whose per-dispatch FETCH_SIZE/WRITE_SIZE of
 the copy (known bytes) calibrate the attention kernel's HBM traffic.
+
+`--summarize RUN_DIR --workloads a,b --out profiles/X.md --title T --trace-cmd C --pmc-cmd C`
+turns such passes into a profile summary (no GPU needed): RUN_DIR/trace holds the
+`rocprofv3 --kernel-trace --stats -o bench` CSVs of a benchmark run, RUN_DIR/pmc_<workload>_<first
+counter>/run_counter_collection.csv the counter passes of `--profile <workload>` (FETCH_SIZE,
+WRITE_SIZE, and SQ_VALU_MFMA_BUSY_CYCLES with the other SQ/GRBM counters of the table). The HBM
+bytes per launch of every workload go to profiles/hbm_traffic.json, stamped with the digest of the
+kernel sources, which `roofline.traffic` reads back.
 """
 
 from __future__ import annotations
@@ -492,6 +500,113 @@ def profile_run(workload: str, launches: int) -> int:
     return 0
 
 
+def summarize(run: str, workloads: list[str], out_md: str, title: str, trace_cmd: str, pmc_cmd: str,
+              trace_filter: str = "") -> int:
+    """Profile summary (markdown) of a rocprofv3 run directory, and the HBM bytes per launch of each
+    workload into profiles/hbm_traffic.json (see the module docstring for the layout)."""
+    import csv
+    import glob
+    import statistics
+
+    cus, simds, xcds = 256, 1024, 8
+    med = statistics.median
+
+    def clean(name: str) -> str:
+        return name.replace("(anonymous namespace)::", "").replace("void ", "").replace("sa::", "").split("(")[0]
+
+    lines = [title, "", "Commands (from the repository root on the MI355X box; rocprofv3 run from /tmp with "
+             "TMPDIR=/tmp):", "", "```", trace_cmd, pmc_cmd, "```", ""]
+    stats_path = os.path.join(run, "trace", "bench_kernel_stats.csv")
+    if os.path.exists(stats_path):
+        lines += ["## Kernel trace (`--kernel-trace --stats` over the benchmark), average duration per kernel", "",
+                  "| kernel | calls | avg us | min us | max us | share |", "|---|---|---|---|---|---|"]
+        for r in csv.DictReader(open(stats_path)):
+            if trace_filter and trace_filter not in r["Name"]:
+                continue
+            lines.append(f"| `{clean(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                         f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.1f}% |")
+        groups: dict = {}
+        for r in csv.DictReader(open(os.path.join(run, "trace", "bench_kernel_trace.csv"))):
+            if "sa::" not in r["Kernel_Name"] or (trace_filter and trace_filter not in r["Kernel_Name"]):
+                continue
+            key = (clean(r["Kernel_Name"]), int(r["Grid_Size_X"]) // int(r["Workgroup_Size_X"]))
+            groups.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        lines += ["", "### The same trace by launch shape (workgroups per launch)", "",
+                  "| kernel | workgroups | calls | avg us | min us | max us |", "|---|---|---|---|---|---|"]
+        for (k, wg), d in sorted(groups.items(), key=lambda kv: -sum(kv[1]))[:14]:
+            lines.append(f"| `{k}` | {wg} | {len(d)} | {sum(d) / len(d):.1f} | {min(d):.1f} | {max(d):.1f} |")
+    pmc: dict = {}
+    for f in sorted(glob.glob(os.path.join(run, "pmc_*", "run_counter_collection.csv"))):
+        tag = os.path.basename(os.path.dirname(f))[4:]
+        wl = next((w for w in workloads if tag.startswith(w + "_")), None)
+        if wl is None:
+            continue
+        for r in csv.DictReader(open(f)):
+            name = r["Kernel_Name"]
+            if "copyBuffer" in name and int(r["Grid_Size"]) > 100000:
+                key = "copy"
+            elif "sa::" in name:
+                key = clean(name)
+            else:
+                continue
+            d = pmc.setdefault(wl, {}).setdefault(key, {})
+            d.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+            d.setdefault("dur", []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    lines += ["", "## Counters per dispatch (median over the launches); HBM bytes calibrated with a 256 MiB copy", "",
+              "| workload | kernel | avg us (counter runs) | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM MB (cal.) | "
+              "MFMA FLOP (MOPS_F32 x 512) | MFMA busy | LDS bank conflicts / LDS active | mean waves/CU |",
+              "|---|---|---|---|---|---|---|---|---|---|"]
+    tj = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    traffic = {}
+    if os.path.exists(tj):
+        with open(tj) as f:
+            traffic = json.load(f)
+        if traffic.get("sources_sha256") != kernel_sources_digest():
+            traffic = {}  # figures of other kernel sources are dropped, not mixed in
+    cal = None
+    for wl in workloads:
+        d = pmc.get(wl)
+        if not d or "copy" not in d:
+            print(f"no counter passes for {wl} under {run}", file=sys.stderr)
+            return 1
+        c = d["copy"]
+        fcal = COPY_BYTES / 1024 / med(c["FETCH_SIZE"])
+        wcal = COPY_BYTES / 1024 / med(c["WRITE_SIZE"])
+        cal = cal or (med(c["FETCH_SIZE"]), med(c["WRITE_SIZE"]))
+        total = 0.0
+        for k, a in d.items():
+            if k == "copy":
+                continue
+            fetch, write = med(a["FETCH_SIZE"]), med(a["WRITE_SIZE"])
+            hbm = (fetch * fcal + write * wcal) * 1024
+            total += hbm
+            if "GRBM_GUI_ACTIVE" in a:
+                grbm = med(a["GRBM_GUI_ACTIVE"]) / xcds
+                util = f"{100 * med(a['SQ_VALU_MFMA_BUSY_CYCLES']) / simds / grbm:.1f}%"
+                mops = f"{med(a['SQ_INSTS_VALU_MFMA_MOPS_F32']) * 512:.4g}"
+                lds = f"{med(a['SQ_LDS_BANK_CONFLICT']):.0f} / {med(a['SQ_LDS_IDX_ACTIVE']):.0f}"
+                waves = f"{4 * med(a['SQ_WAVE_CYCLES']) / grbm / cus:.1f}"
+            else:
+                util = mops = lds = waves = "-"
+            lines.append(f"| {wl} | `{k}` | {med(a['dur']):.1f} | {fetch:.0f} | {write:.0f} | {hbm / 1e6:.1f} | "
+                         f"{mops} | {util} | {lds} | {waves} |")
+        traffic[wl] = {"kernels": [k for k in d if k != "copy"], "bytes_per_launch": round(total),
+                       "fetch_factor": round(fcal, 4), "write_factor": round(wcal, 4)}
+    lines += ["", f"Calibration: the runtime's copy kernel moving {COPY_BYTES} bytes reads FETCH_SIZE = {cal[0]:.1f} KiB "
+              f"and WRITE_SIZE = {cal[1]:.1f} KiB per dispatch, so HBM bytes = FETCH_SIZE x 1024 x "
+              f"{COPY_BYTES / 1024 / cal[0]:.3f} + WRITE_SIZE x 1024 x {COPY_BYTES / 1024 / cal[1]:.3f}.",
+              "MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x GRBM_GUI_ACTIVE / 8 XCDs); mean waves/CU = "
+              "4 x SQ_WAVE_CYCLES / (GRBM_GUI_ACTIVE / 8) / 256.",
+              f"Kernel sources: sha256 {kernel_sources_digest()[:16]}... (`bench.py` `kernel_sources_digest`).", ""]
+    with open(out_md, "w") as f:
+        f.write("\n".join(lines))
+    traffic["sources_sha256"] = kernel_sources_digest()
+    with open(tj, "w") as f:
+        json.dump(traffic, f, indent=1, sort_keys=True)
+    print("\n".join(lines))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -502,7 +617,17 @@ def main() -> int:
     ap.add_argument("--calls", type=int, default=200, help="calls per single-config timing")
     ap.add_argument("--profile", default=None, help="launch only this workload (for rocprofv3 counter passes)")
     ap.add_argument("--launches", type=int, default=20)
+    ap.add_argument("--summarize", default=None, metavar="RUN_DIR", help="write a profile summary (no GPU)")
+    ap.add_argument("--workloads", default="", help="--summarize: comma-separated workloads of the counter passes")
+    ap.add_argument("--out", default=None, help="--summarize: the markdown file to write")
+    ap.add_argument("--title", default="", help="--summarize: first line of the summary")
+    ap.add_argument("--trace-cmd", default="", help="--summarize: the kernel-trace command, quoted in the summary")
+    ap.add_argument("--pmc-cmd", default="", help="--summarize: the counter-pass command, quoted in the summary")
+    ap.add_argument("--trace-filter", default="", help="--summarize: keep trace rows whose kernel name has this")
     args = ap.parse_args()
+    if args.summarize:
+        return summarize(args.summarize, [w for w in args.workloads.split(",") if w], args.out, args.title,
+                         args.trace_cmd, args.pmc_cmd, args.trace_filter)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this operator's path has no multi-GPU form here (asked for --gpus {args.gpus}); "
               "the per-GPU shard of a sharded run is the same kernel at the shapes measured with --gpus 1.",
