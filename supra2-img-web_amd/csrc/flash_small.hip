@@ -319,7 +319,8 @@ __global__ __launch_bounds__(64 * NW, 1) void flash_small_kernel(FlashArgs p) {
     }
     const float inv = lsum > 0.f ? __builtin_amdgcn_rcpf(lsum) : 0.f;  // v_rcp_f32 (1 ulp)
     acc *= inv;
-    if (q0 + q < p.Lq) *reinterpret_cast<f32x4*>(obase + (int64_t)(q0 + q) * p.ldo + 4 * c) = acc;
+    // non-temporal, as in the flash kernel: O is not read again here
+    if (q0 + q < p.Lq) __builtin_nontemporal_store(acc, reinterpret_cast<f32x4*>(obase + (int64_t)(q0 + q) * p.ldo + 4 * c));
   }
 }
 
