@@ -170,10 +170,10 @@ typedef struct sa_attn_plan {
   int64_t workspace_bytes; /* sa_attention_workspace_bytes(args) */
   const char* name;        /* sa_attention_kernel_name(args) (static storage) */
   /* FLASH launches of more units (query tiles) than fit the GPU at once whose last round holds
-   * few units (at most one small-launch workgroup per CU for them): those last units run in a
-   * second launch of the small-launch kernel, split by keys over tail_key_split waves per 32
-   * queries. tail_kernel is SA_KERNEL_FLASH_SMALL then (0 when there is no second launch),
-   * tail_workgroups its grid. */
+   * few units: those last units run in a second launch at one workgroup per CU, of the
+   * small-launch kernel (tail_kernel SA_KERNEL_FLASH_SMALL, tail_key_split 4 waves per 32 queries)
+   * or of the flash kernel split by keys over 2 waves per 32 queries (SA_KERNEL_FLASH, 2);
+   * tail_kernel is 0 when there is no second launch, tail_workgroups the second launch's grid. */
   int32_t tail_kernel;
   int32_t tail_key_split;
   int64_t tail_workgroups;

@@ -624,8 +624,9 @@ int sa_attention_plan(const sa_attn_args* args, sa_attn_plan* plan) {
     plan->workgroups = sa::flash_mfma_workgroups(p, c.nsplit, num_cus());
     const int64_t tail = sa::flash_mfma_tail_units(p, c.nsplit, num_cus());
     if (tail > 0) {
-      plan->tail_kernel = SA_KERNEL_FLASH_SMALL;
-      plan->tail_key_split = sa::flash_small_waves(p);
+      const bool small = sa::flash_mfma_tail_kernel(p, c.nsplit, num_cus()) == sa::TAIL_SMALL;
+      plan->tail_kernel = small ? SA_KERNEL_FLASH_SMALL : SA_KERNEL_FLASH;
+      plan->tail_key_split = small ? sa::flash_small_waves(p) : 2;
       int64_t first = 0;
       plan->tail_workgroups = sa::flash_mfma_tail_groups(p, c.nsplit, num_cus(), &first);
     }

@@ -124,7 +124,9 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
   const int half = lane >> 5;
 
   const int q_tiles = (p.Lq + QT - 1) / QT;
+  // the key-split kernels also run the leftover units of a larger launch: aux is then the first unit
   int tile = xcd_remap(blockIdx.x, p.tiles);
+  if constexpr (NSPLIT > 1 && MASK != MASK_KEY_MASK) tile += p.aux;
   const int qtile = tile % q_tiles;
   tile /= q_tiles;
   const int h = tile % p.H;
@@ -541,7 +543,16 @@ hipError_t launch_split(const AttnParams& p, int num_cus, hipStream_t stream) {
   if (e != hipSuccess || tail == 0) return e;
   int64_t first = 0;
   const int64_t count = flash_mfma_tail_groups(p, NSPLIT, num_cus, &first);
-  return launch_flash_small_groups(p, first, count, stream);
+  if (flash_mfma_tail_kernel(p, NSPLIT, num_cus) == TAIL_SMALL) return launch_flash_small_groups(p, first, count, stream);
+  // 64-query units of the 2-way key-split kernel, from unit `first` on
+  FlashArgs b = flash_args(p, count);
+  b.aux = (int32_t)first;
+  const dim3 tgrid((unsigned)count);
+  if constexpr (D == 64) {
+    if (p.mask_mode == MASK_NONE) return launch_one<64, 2, BIAS_NONE, MASK_NONE>(b, p, tgrid, num_cus, stream);
+    return launch_one<64, 2, BIAS_NONE, MASK_KEY_LEN>(b, p, tgrid, num_cus, stream);
+  }
+  return hipErrorInvalidValue;
 }
 
 }  // namespace
@@ -613,10 +624,12 @@ FlashVariant flash_mfma_variant(const AttnParams& p, int nsplit) {
 // The 4-per-CU kernels run a launch of more units than that in rounds. Units past the last whole
 // round start only as the first workgroups finish and then run at one wave per SIMD: the batch-56
 // DiT self-attention call (1008 units of 128 queries) took 69.5 us, the batch-57 one (1026 units)
-// 83.9 us. When the units left over fit flash_small at one workgroup (4 waves, 32 queries each) per
-// CU, they go there instead, in a second launch right after this one: batch 57 then took 78.9 us,
-// batch 60 (56 units left) 79.2 us instead of 85.0. Batch 64 (128 left, two such workgroups per
-// CU) took 86.2 us instead of 84.8 and keeps the single launch.
+// 83.9 us. The units left over go to a second launch right after this one when it runs them at one
+// workgroup per CU: through flash_small (4 waves per 32 queries) when their 32-query groups fit,
+// else through the 2-way key-split flash kernel (64-query units). Measured on one box: batch 57
+// 83.9 -> 77.7-79.6 us, batch 60 (56 units left) 85.0 -> 77.9-79.6 us (flash_small; the split
+// kernel gave 81.6-82.0), batch 64 (128 left) 83.7 -> 82.3 us (split kernel; flash_small at two
+// workgroups per CU gave 86.2).
 int64_t flash_mfma_tail_units(const AttnParams& p, int nsplit, int num_cus) {
   const bool eligible = p.D == 64 && compiled_split(p.D, nsplit) == 1 && p.bias_mode == BIAS_NONE &&
                         (p.mask_mode == MASK_NONE || (p.mask_mode == MASK_KEY_LEN && p.order_n == 0)) && p.Lk > 32;
@@ -625,7 +638,13 @@ int64_t flash_mfma_tail_units(const AttnParams& p, int nsplit, int num_cus) {
   const int64_t slots = 4 * (int64_t)num_cus;
   if (tiles <= slots) return 0;
   const int64_t rest = tiles % slots;
-  return 4 * rest <= num_cus ? rest : 0;
+  return 2 * rest <= num_cus ? rest : 0;
+}
+
+int flash_mfma_tail_kernel(const AttnParams& p, int nsplit, int num_cus) {
+  const int64_t tail = flash_mfma_tail_units(p, nsplit, num_cus);
+  if (tail == 0) return TAIL_NONE;
+  return 4 * tail <= num_cus ? TAIL_SMALL : TAIL_SPLIT2;
 }
 
 int64_t flash_mfma_tail_groups(const AttnParams& p, int nsplit, int num_cus, int64_t* first) {
@@ -633,11 +652,13 @@ int64_t flash_mfma_tail_groups(const AttnParams& p, int nsplit, int num_cus, int
   *first = 0;
   if (tail == 0) return 0;
   // unit t = (b*H + h)*q_tiles + qtile holds the 32-query groups from (b*H + h)*q_groups + 4*qtile
-  // on, and the units after it the groups after those
-  const int64_t q_tiles = (p.Lq + 127) / 128, q_groups = (p.Lq + 31) / 32;
+  // on (the 64-query units from (b*H + h)*q_units + 2*qtile), and the units after it the ones after
+  const int64_t q_tiles = (p.Lq + 127) / 128;
+  const int64_t per = flash_mfma_tail_kernel(p, nsplit, num_cus) == TAIL_SMALL ? 4 : 2;  // sub-units per unit
+  const int64_t q_sub = (p.Lq + 128 / per - 1) / (128 / per);
   const int64_t t = (int64_t)p.B * p.H * q_tiles - tail;
-  *first = (t / q_tiles) * q_groups + 4 * (t % q_tiles);
-  return (int64_t)p.B * p.H * q_groups - *first;
+  *first = (t / q_tiles) * q_sub + per * (t % q_tiles);
+  return (int64_t)p.B * p.H * q_sub - *first;
 }
 
 int64_t flash_mfma_workgroups(const AttnParams& p, int nsplit, int num_cus) {

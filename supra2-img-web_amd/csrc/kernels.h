@@ -86,9 +86,12 @@ struct FlashVariant {
 FlashVariant flash_mfma_variant(const AttnParams& p, int nsplit);
 // Workgroups of that launch.
 int64_t flash_mfma_workgroups(const AttnParams& p, int nsplit, int num_cus);
-// Units (query tiles) of a flash launch that go to a second, flash_small launch (0 = none), and
-// the 32-query groups [*first, *first + count) they hold (returns count).
+// Units (128-query tiles) of a flash launch that go to a second launch (0 = none), the kernel of
+// that launch, and the work items [*first, *first + count) it runs (returns count): 32-query groups
+// of flash_small, or 64-query units of the 2-way key-split flash kernel.
+constexpr int TAIL_NONE = 0, TAIL_SMALL = 1, TAIL_SPLIT2 = 2;
 int64_t flash_mfma_tail_units(const AttnParams& p, int nsplit, int num_cus);
+int flash_mfma_tail_kernel(const AttnParams& p, int nsplit, int num_cus);
 int64_t flash_mfma_tail_groups(const AttnParams& p, int nsplit, int num_cus, int64_t* first);
 // 32-query groups [first, first + count) of the call through flash_small_kernel (no key mask).
 hipError_t launch_flash_small_groups(const AttnParams& p, int64_t first, int64_t count, hipStream_t stream);

@@ -107,26 +107,27 @@ def big(B, Lq=256, **over):
     return good_args(B=B, Lq=Lq, sq=Lq * 1728, so=Lq * 576, o=FAKE + (1 << 36), **over)
 
 
-@pytest.mark.parametrize("B,Lq,tail_units,tail_groups", [
-    (56, 256, 0, 0),      # 1008 units: one round on 256 CUs
-    (57, 256, 2, 8),      # 1026: a round of 1024 and two left
-    (60, 256, 56, 224),   # 1080: 56 left, 224 groups of 32 queries
-    (61, 256, 0, 0),      # 1098: 74 left would need 296 small workgroups: one launch
-    (64, 256, 0, 0),      # the batch-64 DiT call: 128 left, one launch
-    (114, 256, 4, 16),    # 2052: two whole rounds and four left
-    (57, 200, 2, 7),      # 7 groups of 32 per head: the tail is one whole head of 2 units
+SMALL, FLASH = _lib.SA_KERNEL_FLASH_SMALL, _lib.SA_KERNEL_FLASH
+
+
+@pytest.mark.parametrize("B,Lq,tail_units,tail_kernel,tail_split,tail_wg", [
+    (56, 256, 0, 0, 0, 0),          # 1008 units: one round on 256 CUs
+    (57, 256, 2, SMALL, 4, 8),      # 1026: a round of 1024, two left: 8 groups of 32 queries
+    (60, 256, 56, SMALL, 4, 224),   # 1080: 56 left, 224 groups
+    (61, 256, 74, FLASH, 2, 148),   # 1098: 74 left, 296 groups would not fit: 148 units of 64 queries
+    (64, 256, 128, FLASH, 2, 256),  # the batch-64 DiT call: 128 left, 256 units of 64 queries
+    (71, 256, 0, 0, 0, 0),          # 1278: 254 left would need more than one workgroup per CU: one launch
+    (114, 256, 4, SMALL, 4, 16),    # 2052: two whole rounds and four left
+    (57, 200, 2, SMALL, 4, 7),      # 7 groups of 32 per head: the tail is one whole head of 2 units
+    (61, 200, 74, FLASH, 2, 148),   # 4 units of 64 per head (the last one 8 queries)
 ])
-def test_plan_reports_the_tail_launch(B, Lq, tail_units, tail_groups):
+def test_plan_reports_the_tail_launch(B, Lq, tail_units, tail_kernel, tail_split, tail_wg):
     """The batch-B, 9-head self-attention call on 256 CUs (the count without a device): the units past
-    the last whole round of 1024 go to flash_small when they fit it at one workgroup per CU."""
+    the last whole round of 1024 go to a second launch when it runs them at one workgroup per CU."""
     plan = _lib.plan(big(B, Lq))
     assert plan.kernel == _lib.SA_KERNEL_FLASH and plan.name == b"flash_mfma_d64"
     assert plan.workgroups == B * 9 * ((Lq + 127) // 128) - tail_units
-    if tail_units:
-        assert (plan.tail_kernel, plan.tail_key_split, plan.tail_workgroups) == (_lib.SA_KERNEL_FLASH_SMALL, 4,
-                                                                                  tail_groups)
-    else:
-        assert (plan.tail_kernel, plan.tail_workgroups) == (0, 0)
+    assert (plan.tail_kernel, plan.tail_key_split, plan.tail_workgroups) == (tail_kernel, tail_split, tail_wg)
 
 
 @pytest.mark.parametrize("over", [

@@ -1,7 +1,7 @@
-"""GPU parity of flash launches whose last round goes to the small-launch kernel: more units
-(128-query tiles) than the 4-per-CU kernel holds at once, with few enough left over for one
-small-launch workgroup per CU.
-The first launch covers the leading units, flash_small the 32-query groups of the rest; every
+"""GPU parity of flash launches whose last round goes to a second launch: more units (128-query
+tiles) than the 4-per-CU kernel holds at once, with few enough left over for one workgroup per CU
+of the small-launch kernel (32-query groups) or of the 2-way key-split flash kernel (64-query units).
+The first launch covers the leading units, the second the rest; every
 output row is checked against the PyTorch fp32 CPU path and the float64 brute force (1e-5)."""
 
 from __future__ import annotations
@@ -24,15 +24,18 @@ def tail_units(call) -> int:
     cus = 256  # MI355X
     tiles = call.B * call.H * ((call.Lq + 127) // 128)
     rest = tiles % (4 * cus)
-    return rest if tiles > 4 * cus and 4 * rest <= cus else 0
+    return rest if tiles > 4 * cus and 2 * rest <= cus else 0
 
 
 @pytest.mark.parametrize("B,Lq,Lk,mask", [
-    (57, 256, 256, "none"),      # 1026 units: a tail of two
+    (57, 256, 256, "none"),      # 1026 units: a tail of two (small-launch kernel)
     (60, 256, 256, "none"),      # 1080 units: a tail of 56 (224 small workgroups)
     (60, 250, 250, "none"),      # ragged
     (57, 200, 230, "none"),      # 7 groups of 32 per (b, h): the tail starts inside a head
     (60, 256, 256, "key_len"),   # per-sequence key lengths (launch order, no host copy)
+    (64, 256, 256, "none"),      # the batch-64 DiT call: 128 left, 2-way key-split flash kernel
+    (61, 200, 230, "none"),      # 74 left, split kernel, ragged 64-query units
+    (64, 256, 256, "key_len"),   # split kernel with key lengths
 ])
 def test_tail_launch_parity(dev, B, Lq, Lk, mask):
     kl = None
@@ -53,7 +56,9 @@ def test_tail_launch_parity(dev, B, Lq, Lk, mask):
         n_tail = tail_units(call)
         assert n_tail > 0
         assert plan.workgroups == B * 9 * ((Lq + 127) // 128) - n_tail
-        assert plan.tail_kernel == _lib.SA_KERNEL_FLASH_SMALL and plan.tail_key_split == 4
+        small = 4 * n_tail <= 256
+        assert (plan.tail_kernel, plan.tail_key_split) == ((_lib.SA_KERNEL_FLASH_SMALL, 4) if small
+                                                           else (_lib.SA_KERNEL_FLASH, 2))
         out = st.run()
     finally:
         st.release()
