@@ -341,7 +341,11 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
 #pragma unroll
       for (int r = 1; r < 16; ++r) mb = max_nan(mb, u[r]);
       mb = max_with_partner(mb);
-      if (__builtin_amdgcn_ballot_w64(mb > m + kRescaleSlack) != 0) {
+      if (step == 0) {
+        // the wave's first block: its maximum becomes the reference (O and l are still zero, so there is
+        // nothing to rescale; -FLT_MAX stays for rows with every key masked)
+        m = max_nan(m, mb);
+      } else if (__builtin_amdgcn_ballot_w64(mb > m + kRescaleSlack) != 0) {
         const float m_new = max_nan(m, mb);
         const float alpha = fast_exp2(m - m_new);
         m = m_new;
@@ -549,8 +553,7 @@ hipError_t launch_split(const AttnParams& p, int num_cus, hipStream_t stream) {
   b.aux = (int32_t)first;
   const dim3 tgrid((unsigned)count);
   if constexpr (D == 64) {
-    if (p.mask_mode == MASK_NONE) return launch_one<64, 2, BIAS_NONE, MASK_NONE>(b, p, tgrid, num_cus, stream);
-    return launch_one<64, 2, BIAS_NONE, MASK_KEY_LEN>(b, p, tgrid, num_cus, stream);
+    return launch_one<64, 2, BIAS_NONE, MASK_NONE>(b, p, tgrid, num_cus, stream);
   }
   return hipErrorInvalidValue;
 }
@@ -631,8 +634,11 @@ FlashVariant flash_mfma_variant(const AttnParams& p, int nsplit) {
 // kernel gave 81.6-82.0), batch 64 (128 left) 83.7 -> 82.3 us (split kernel; flash_small at two
 // workgroups per CU gave 86.2).
 int64_t flash_mfma_tail_units(const AttnParams& p, int nsplit, int num_cus) {
+  // Unmasked calls only: with key lengths, the second launch would run a call's last units through
+  // other arithmetic depending on whether a host copy of the lengths (the schedule) came with it,
+  // and the schedule must leave the result bit for bit unchanged.
   const bool eligible = p.D == 64 && compiled_split(p.D, nsplit) == 1 && p.bias_mode == BIAS_NONE &&
-                        (p.mask_mode == MASK_NONE || (p.mask_mode == MASK_KEY_LEN && p.order_n == 0)) && p.Lk > 32;
+                        p.mask_mode == MASK_NONE && p.Lk > 32;
   if (!eligible) return 0;
   const int64_t tiles = (int64_t)p.B * p.H * ((p.Lq + 127) / 128);
   const int64_t slots = 4 * (int64_t)num_cus;

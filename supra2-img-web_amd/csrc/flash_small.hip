@@ -228,7 +228,11 @@ __global__ __launch_bounds__(64 * NW, 1) void flash_small_kernel(FlashArgs p) {
 #pragma unroll
     for (int r = 1; r < 16; ++r) mb = max_nan(mb, u[r]);
     mb = max_with_partner(mb);
-    if (__builtin_amdgcn_ballot_w64(mb > m + kRescaleSlack) != 0) {
+    if (j == blk0) {
+      // the wave's first block: its maximum becomes the reference (O and l are still zero, so there is
+      // nothing to rescale; -FLT_MAX stays for rows with every key masked)
+      m = max_nan(m, mb);
+    } else if (__builtin_amdgcn_ballot_w64(mb > m + kRescaleSlack) != 0) {
       const float m_new = max_nan(m, mb);
       const float alpha = fast_exp2(m - m_new);
       m = m_new;

@@ -134,7 +134,8 @@ def test_plan_reports_the_tail_launch(B, Lq, tail_units, tail_kernel, tail_split
     dict(bias_mode=1, bias=FAKE + (3 << 36)),                 # a dense bias
     dict(mask_mode=2, key_mask=FAKE + (3 << 36), smask=256),  # a key mask
     dict(Lk=32, sk=32 * 1728, sv=32 * 1728),                  # one key block
-])
+    dict(mask_mode=1, key_len=FAKE + (3 << 36)),              # key lengths: the result may not depend on
+])                                                            # whether the schedule's host copy comes along
 def test_no_tail_launch_outside_the_plain_variants(over):
     plan = _lib.plan(big(60, **over))
     assert plan.kernel == _lib.SA_KERNEL_FLASH and plan.tail_kernel == 0
