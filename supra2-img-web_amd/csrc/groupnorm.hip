@@ -14,6 +14,7 @@
 // Both read and write float4 items when the group width, C and the pointers allow it.
 
 #include <algorithm>
+#include <type_traits>
 #include <stdint.h>
 
 #include "common.h"
@@ -75,17 +76,32 @@ __global__ __launch_bounds__(256) void groupnorm_stats_kernel(const float* __res
   const int64_t items = (int64_t)np * w;
   const int64_t n = (int64_t)np * cg;
   const float* base = x + (int64_t)p0 * C + g * cg;
-  float acc = 0.f;
-  for (int64_t i = threadIdx.x; i < items; i += 256) {
+  auto item = [&](int64_t i) {
     const int64_t pix = i / w;
-    acc += item_sum<VEC>(base + pix * C + (VEC ? 4 : 1) * (i - pix * w));
+    return base + pix * C + (VEC ? 4 : 1) * (i - pix * w);
+  };
+  // The thread's first KEEP items stay in registers for the centred pass (a chunk of the VAE
+  // image is one item per thread); later ones are read again.
+  constexpr int KEEP = 4;
+  using Item = typename std::conditional<VEC, f32x4, float>::type;
+  Item kept[KEEP];
+  float acc = 0.f;
+#pragma unroll
+  for (int k = 0; k < KEEP; ++k) {
+    const int64_t i = threadIdx.x + 256 * k;
+    if (i < items) {
+      kept[k] = *reinterpret_cast<const Item*>(item(i));
+      acc += item_sum<VEC>(reinterpret_cast<const float*>(&kept[k]));
+    }
   }
+  for (int64_t i = threadIdx.x + 256 * KEEP; i < items; i += 256) acc += item_sum<VEC>(item(i));
   const float mean = n > 0 ? block_sum(acc, red) / (float)n : 0.f;
   float m2 = 0.f;
-  for (int64_t i = threadIdx.x; i < items; i += 256) {
-    const int64_t pix = i / w;
-    m2 += item_sq<VEC>(base + pix * C + (VEC ? 4 : 1) * (i - pix * w), mean);
+#pragma unroll
+  for (int k = 0; k < KEEP; ++k) {
+    if (threadIdx.x + 256 * k < items) m2 += item_sq<VEC>(reinterpret_cast<const float*>(&kept[k]), mean);
   }
+  for (int64_t i = threadIdx.x + 256 * KEEP; i < items; i += 256) m2 += item_sq<VEC>(item(i), mean);
   m2 = n > 0 ? block_sum(m2, red) : 0.f;
   if (threadIdx.x == 0) {
     part[3 * blockIdx.x + 0] = (float)n;
@@ -108,6 +124,25 @@ __global__ __launch_bounds__(256) void groupnorm_apply_kernel(const float* __res
   extern __shared__ float sm[];  // [G][2]: mean, rstd; then (STAGED) the [G*S][3] chunk statistics
   float* stats = sm;
   const float* src = part;
+  const int w = VEC ? C / 4 : C;  // items per pixel row
+  const int64_t total = (int64_t)HW * w;
+  const int64_t i0 = (int64_t)blockIdx.x * per_block;
+  const int64_t i1 = min(total, i0 + per_block);
+  // The thread's first item (and its gamma, beta) is loaded before the statistics are combined, so
+  // the two memory round trips overlap instead of running one after the other.
+  using Item = typename std::conditional<VEC, f32x4, float>::type;
+  const int64_t ifirst = i0 + threadIdx.x;
+  Item v0{}, ga0{}, be0{};
+  int64_t e0 = 0;
+  int c0 = 0;
+  if (ifirst < i1) {
+    const int64_t row = ifirst / w;
+    c0 = (VEC ? 4 : 1) * (int)(ifirst - row * w);
+    e0 = row * C + c0;
+    v0 = *reinterpret_cast<const Item*>(x + e0);
+    ga0 = *reinterpret_cast<const Item*>(gamma + c0);
+    be0 = *reinterpret_cast<const Item*>(beta + c0);
+  }
   if constexpr (STAGED) {
     float* staged = sm + 2 * G;
     for (int i = threadIdx.x; i < 3 * G * S; i += 256) staged[i] = part[i];
@@ -130,11 +165,19 @@ __global__ __launch_bounds__(256) void groupnorm_apply_kernel(const float* __res
     stats[2 * g + 1] = rsqrtf(m2 / n + eps);
   }
   __syncthreads();
-  const int w = VEC ? C / 4 : C;  // items per pixel row
-  const int64_t total = (int64_t)HW * w;
-  const int64_t i0 = (int64_t)blockIdx.x * per_block;
-  const int64_t i1 = min(total, i0 + per_block);
-  for (int64_t i = i0 + threadIdx.x; i < i1; i += 256) {
+  if (ifirst < i1) {
+    const int g = c0 / cg;  // with VEC the four channels share a group (cg % 4 == 0)
+    const float mean = stats[2 * g], rstd = stats[2 * g + 1];
+    if constexpr (VEC) {
+      f32x4 o;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) o[k] = fmaf((v0[k] - mean) * rstd, ga0[k], be0[k]);
+      *reinterpret_cast<f32x4*>(y + e0) = o;
+    } else {
+      y[e0] = fmaf((v0 - mean) * rstd, ga0, be0);
+    }
+  }
+  for (int64_t i = ifirst + 256; i < i1; i += 256) {
     const int64_t row = i / w;
     const int c = (VEC ? 4 : 1) * (int)(i - row * w);
     const int g = c / cg;  // with VEC the four channels share a group (cg % 4 == 0)
