@@ -337,6 +337,143 @@ __global__ __launch_bounds__(256, 2) void linear_mfma_kernel(LinearParams p, Til
   }
 }
 
+// Small products (fewer 64 x 64 tiles than two per CU: the VAE projections, batch-2 DiT calls): one
+// workgroup per 32 x 32 output tile, its four waves on different k of the same tile. K advances in
+// 64-deep tiles of 8 groups of 8; wave w multiplies groups 2w and 2w + 1 (8 MFMAs per tile), so a
+// wave's MFMA chain is a quarter of K and the short grids spread over many more SIMDs. The four
+// partial sums meet in LDS, and wave w adds them up (in wave order) for rows 8w + 4*half + 0..3 of
+// the tile and runs the epilogue for those rows. Copies, swizzle and the clamped last k-tile as in
+// linear_mfma_kernel.
+template <int ACT, int EPI>
+__global__ __launch_bounds__(256) void linear_ksplit_kernel(LinearParams p, TileOrder order) {
+  constexpr int BM = 32, BN = 32, BK = 64, NS = 2;
+  constexpr int CPR = BK / 4;  // 16-byte chunks per tile row
+  constexpr int NG = BK / 8;   // groups of 8 k per tile, two per wave
+  constexpr int A_TILE = BM * BK;
+  constexpr int STAGE = (BM + BN) * BK;
+  constexpr int NI = BM * CPR / 256;  // DMA instructions per wave, tensor and stage
+  static_assert(NI * 256 == BM * CPR && BM == BN, "tiles must split into whole wave copies");
+
+  __shared__ __attribute__((aligned(16))) float lds[NS * STAGE];  // 32 KiB; the partial sums reuse it
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31;
+  const int half = lane >> 5;
+
+  int mi, ni;
+  tile_coords(xcd_remap(blockIdx.x, order.tiles_m * order.tiles_n), order, mi, ni);
+  const int m0 = mi * BM;
+  const int n0 = ni * BN;
+  const int mlast = min(BM, p.M - m0) - 1;
+  const int nlast = min(BN, p.N - n0) - 1;
+
+  // chunk of DMA instruction n: physical chunk (n*4 + wave)*64 + lane, row pc / CPR, logical chunk
+  // c at physical c ^ (row % CPR)
+  unsigned aoff[NI], boff[NI];
+  int ccol[NI];
+#pragma unroll
+  for (int n = 0; n < NI; ++n) {
+    const int pc_all = (n * 4 + wave) * 64 + lane;
+    const int row = pc_all / CPR;
+    const int c = (pc_all % CPR) ^ (row % CPR);
+    ccol[n] = 4 * c;
+    aoff[n] = 4u * (unsigned)(min(row, mlast) * (int)p.ldx + 4 * c);
+    boff[n] = 4u * (unsigned)(min(row, nlast) * (int)p.ldw + 4 * c);
+  }
+  const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(p.x + p.x_off + (int64_t)m0 * p.ldx);
+  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(p.w + (int64_t)n0 * p.ldw);
+  const int nkt = (p.K + BK - 1) / BK;
+  const int nfull = p.K / BK;
+  auto issue = [&](int kt, auto stage) {
+    constexpr int S = decltype(stage)::value;
+    float* at = lds + S * STAGE;
+    float* bt = at + A_TILE;
+    if (kt < nfull) {
+      const unsigned soff = 4u * (unsigned)(kt * BK);
+#pragma unroll
+      for (int n = 0; n < NI; ++n) {
+        buffer_to_lds16(xr, aoff[n], at + (n * 4 + wave) * 256, soff);
+        buffer_to_lds16(wr, boff[n], bt + (n * 4 + wave) * 256, soff);
+      }
+    } else {
+      // the tile holding K: columns at or past K re-read the last group (never multiplied)
+      const int k0 = nfull * BK;
+      const unsigned soff = 4u * (unsigned)k0;
+      const int kmax = p.K - 8 - k0;
+#pragma unroll
+      for (int n = 0; n < NI; ++n) {
+        const unsigned shift = 4u * (unsigned)(ccol[n] > kmax + 4 ? (ccol[n] & ~7) - kmax : 0);
+        buffer_to_lds16(xr, aoff[n] - shift, at + (n * 4 + wave) * 256, soff);
+        buffer_to_lds16(wr, boff[n] - shift, bt + (n * 4 + wave) * 256, soff);
+      }
+    }
+  };
+
+  f32x16 acc = zero16();
+  const int swz = col % CPR;
+  auto step = [&](int kt, auto stage) {
+    constexpr int S = decltype(stage)::value;
+    wait_vmcnt<0>();
+    __syncthreads();  // tile kt is whole, and every wave is done with the stage the next copy fills
+    if (kt + 1 < nkt) issue(kt + 1, std::integral_constant<int, S ^ 1>{});
+    const int ng = kt < nfull ? NG : (p.K - nfull * BK) >> 3;  // valid groups of 8 k in this tile
+    const float* at = lds + S * STAGE + col * BK;
+    const float* bt = lds + S * STAGE + A_TILE + col * BK;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int g = 2 * wave + u;
+      if (g < ng) {
+        const int c = 4 * ((2 * g + half) ^ swz);
+        const f32x4 ra = *reinterpret_cast<const f32x4*>(at + c);
+        const f32x4 rb = *reinterpret_cast<const f32x4*>(bt + c);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(ra[s], rb[s], acc, 0, 0, 0);
+      }
+    }
+  };
+  issue(0, std::integral_constant<int, 0>{});
+  int kt = 0;
+  for (; kt + 2 <= nkt; kt += 2) {
+    step(kt, std::integral_constant<int, 0>{});
+    step(kt + 1, std::integral_constant<int, 1>{});
+  }
+  if (kt < nkt) step(kt, std::integral_constant<int, 0>{});
+
+  // ---- partial sums through LDS: wave w's register r of lane l at red[(w*16 + r)*64 + l]
+  __syncthreads();  // every wave is done with the tiles
+  float* red = lds;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) red[(wave * 16 + r) * 64 + lane] = acc[r];
+  __syncthreads();
+  // ---- epilogue: wave w finishes registers 4w..4w+3 = rows 8w + 4*half + 0..3 of column n0 + col
+  const int n = n0 + col;
+  if (n >= p.N) return;
+  const float bias_n = p.bias ? p.bias[n] : 0.f;
+  float gate_n = 1.f;
+  if constexpr (EPI == LIN_EPI_RESID_GATE) gate_n = p.gate[p.gate_off + n];
+  const float* rsrc = p.resid ? p.resid : p.y;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int r = 4 * wave + k;
+    const int m = m0 + 8 * wave + 4 * half + k;
+    if (m < p.M) {
+      float sum = red[r * 64 + lane];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) sum += red[(w * 16 + r) * 64 + lane];
+      float v = apply_act<ACT>(fmaf(sum, p.alpha, bias_n));
+      const int64_t e = p.y_off + (int64_t)m * p.ldy + n;
+      if constexpr (EPI != LIN_EPI_STORE) v = fmaf(gate_n, v, rsrc[e]);
+      if constexpr (EPI == LIN_EPI_STORE) {
+        __builtin_nontemporal_store(v, p.y + e);  // not read back here, as in linear_mfma_kernel
+      } else {
+        p.y[e] = v;
+      }
+    }
+  }
+}
+
 // Any shape and alignment: one thread per output, 16 x 16 outputs per workgroup, K in steps of
 // 16 through LDS. Used when rows are not 16-byte aligned or K % 8 != 0.
 __global__ __launch_bounds__(256) void linear_generic_kernel(LinearParams p) {
@@ -417,6 +554,39 @@ hipError_t launch_epi(const LinearParams& p, hipStream_t stream) {
   }
 }
 
+template <int ACT, int EPI>
+hipError_t launch_ksplit_tiles(const LinearParams& p, hipStream_t stream) {
+  TileOrder o;
+  o.tiles_m = (p.M + 31) / 32;
+  o.tiles_n = (p.N + 31) / 32;
+  o.group_n = o.tiles_n;  // the operands of these small products stay in the L2
+  o.sb_rows = (o.tiles_m + 7) / 8;
+  const int64_t n = (int64_t)o.tiles_m * o.tiles_n;
+  if (n > 0x7fffffff) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL((linear_ksplit_kernel<ACT, EPI>), dim3((unsigned)n), dim3(256), 0, stream, p, o);
+  return hipGetLastError();
+}
+
+template <int ACT>
+hipError_t launch_ksplit_epi(const LinearParams& p, hipStream_t stream) {
+  switch (p.epi) {
+    case LIN_EPI_STORE: return launch_ksplit_tiles<ACT, LIN_EPI_STORE>(p, stream);
+    case LIN_EPI_RESID: return launch_ksplit_tiles<ACT, LIN_EPI_RESID>(p, stream);
+    case LIN_EPI_RESID_GATE: return launch_ksplit_tiles<ACT, LIN_EPI_RESID_GATE>(p, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_ksplit(const LinearParams& p, hipStream_t stream) {
+  switch (p.act) {
+    case LIN_ACT_NONE: return launch_ksplit_epi<LIN_ACT_NONE>(p, stream);
+    case LIN_ACT_GELU: return launch_ksplit_epi<LIN_ACT_GELU>(p, stream);
+    case LIN_ACT_GELU_TANH: return launch_ksplit_epi<LIN_ACT_GELU_TANH>(p, stream);
+    case LIN_ACT_SILU: return launch_ksplit_epi<LIN_ACT_SILU>(p, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 template <int WM, int WN, int BK, int NS>
 hipError_t launch_act(const LinearParams& p, hipStream_t stream) {
   switch (p.act) {
@@ -445,18 +615,25 @@ LinearTile linear_mfma_tile(const LinearParams& p, int num_cus) {
   // 2304-wide fc1 (324 us; 64 x 192: 336 us); 64 x 192 tiles (one 32 x 96 strip per wave, each x
   // operand read feeding three MFMAs) with k-depth 16 and three stages at three workgroups per CU
   // for qkv (245 us; k-depth 32 / two stages 254, 128 x 192 271) and the 576-wide layers (proj/q/
-  // cproj 85-88 us, fc2 320 us; 64 x 64: 90-95 and 337). 64 x 64 tiles spread small calls (the
-  // 1024-row VAE projections, per-prompt context projections, batch-2 calls) over more CUs.
+  // cproj 85-88 us, fc2 320 us; 64 x 64: 90-95 and 337). Grids of fewer 64 x 64 tiles than 1.25
+  // per CU take linear_ksplit_kernel, whose quarter-K waves spread them over the SIMDs (us, 64 x 64
+  // -> k-split: VAE output projection 1024 x 512 x 512 11.75 -> 8.1, context k|v 77 x 1152 x 576 13.2
+  // -> 6.3, batch-2 proj/q/cproj 512 x 576 x 576 12.6-13.0 -> 8.4-8.7, fc1 512 x 2304 x 576 21.4 ->
+  // 19.2, fc2 512 x 576 x 2304 43.4 -> 23.0); wider grids keep 64 x 64 tiles, whose operands are
+  // shared by twice the outputs (VAE q|k|v 1024 x 1536 x 512, 384 tiles: 18.7 against 18.9-19.4).
   const int64_t tiles_wide = ((p.M + 127) / 128) * ((p.N + 191) / 192);
   const int64_t tiles_tall = ((p.M + 63) / 64) * ((p.N + 191) / 192);
-  if (p.N >= 2048 && tiles_wide >= num_cus) return {2, 3, 32, 2};
-  if ((p.N % 192 == 0 || p.N >= 1024) && tiles_tall >= 3 * (int64_t)num_cus) return {1, 3, 16, 3};
-  return {1, 1, 32, 2};
+  const int64_t tiles_64 = ((p.M + 63) / 64) * ((p.N + 63) / 64);
+  if (p.N >= 2048 && tiles_wide >= num_cus) return {2, 3, 32, 2, 0};
+  if ((p.N % 192 == 0 || p.N >= 1024) && tiles_tall >= 3 * (int64_t)num_cus) return {1, 3, 16, 3, 0};
+  if (4 * tiles_64 < 5 * (int64_t)num_cus) return {1, 1, 64, 2, 1};
+  return {1, 1, 32, 2, 0};
 }
 
 const char* linear_kernel_name(const LinearParams& p, int num_cus) {
   if (!linear_mfma_supported(p)) return "linear_generic";
   const LinearTile t = linear_mfma_tile(p, num_cus);
+  if (t.ksplit) return "linear_mfma_32x32_ksplit";
   if (t.wm == 2) return "linear_mfma_128x192";
   if (t.wn == 3) return "linear_mfma_64x192";
   return "linear_mfma_64x64";
@@ -470,6 +647,7 @@ hipError_t launch_linear(const LinearParams& p, int num_cus, hipStream_t stream)
     return hipGetLastError();
   }
   const LinearTile t = linear_mfma_tile(p, num_cus);
+  if (t.ksplit) return launch_ksplit(p, stream);
   if (t.wm == 2) return launch_act<2, 3, 32, 2>(p, stream);
   if (t.wn == 3) return launch_act<1, 3, 16, 3>(p, stream);
   return launch_act<1, 1, 32, 2>(p, stream);

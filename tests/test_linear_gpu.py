@@ -94,6 +94,23 @@ def test_large_tiles_ragged(dev, M, N, K, tile):
     run_checked(dev, call, expect_kernel=f"linear_mfma_{tile}", check_fp64=False)
 
 
+@pytest.mark.parametrize("M,N,K,epi,act,tile", [
+    # k-split 32 x 32 tiles: ragged M and N; K = 64 k-tiles plus a partial tile of 1 or 7 groups of 8
+    (300, 333, 520, _lib.SA_EPI_RESID_GATE, _lib.SA_ACT_GELU_TANH, "32x32_ksplit"),
+    (250, 97, 568, _lib.SA_EPI_RESID, _lib.SA_ACT_SILU, "32x32_ksplit"),
+    (1000, 512, 2304, _lib.SA_EPI_STORE, _lib.SA_ACT_GELU, "32x32_ksplit"),  # long K (288 MFMAs per wave)
+    (33, 1152, 64, _lib.SA_EPI_STORE, _lib.SA_ACT_NONE, "32x32_ksplit"),     # one whole k-tile
+    # 64 x 64 tiles (more than 1.25 tiles per CU, too few for the larger tiles), ragged
+    (2000, 700, 200, _lib.SA_EPI_RESID_GATE, _lib.SA_ACT_NONE, "64x64"),
+])
+def test_small_grid_tiles(dev, M, N, K, epi, act, tile):
+    """The two small-grid tiles: the k-split kernel (the four waves of a workgroup on different k of one
+    32 x 32 tile, partial sums added in LDS, each wave storing a quarter of the rows) and the 64 x 64 tile."""
+    call = make_linear(f"small_{M}x{N}x{K}", M, N, K, seed=M + 3 * N + K, act=act, epi=epi,
+                       gate_off=5 if epi == _lib.SA_EPI_RESID_GATE else 0)
+    run_checked(dev, call, expect_kernel=f"linear_mfma_{tile}")
+
+
 def test_repeat_is_bitwise_identical(dev):
     call = dit_block_linears(B=2)[4]
     st = StagedLinear(dev, call)
