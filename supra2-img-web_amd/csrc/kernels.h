@@ -153,7 +153,7 @@ struct LinearParams {
 struct LinearTile {
   int wm, wn;  // 32x32 accumulators per wave along M and N (tile 64*wm x 64*wn)
   int bk, ns;  // k-tile depth and LDS stages
-  int ksplit;  // 1: linear_ksplit_kernel (32 x 32 tiles, the workgroup's waves on different k)
+  int ksplit;  // k splits of linear_ksplit_kernel (4: 32 x 32 tiles, 2: 32 x 64 tiles), 0: linear_mfma_kernel
 };
 // MFMA kernel when K % 8 == 0 and x, W rows are 16-byte aligned; the generic kernel otherwise.
 bool linear_mfma_supported(const LinearParams& p);

@@ -337,28 +337,37 @@ __global__ __launch_bounds__(256, 2) void linear_mfma_kernel(LinearParams p, Til
   }
 }
 
-// Small products (fewer 64 x 64 tiles than two per CU: the VAE projections, batch-2 DiT calls): one
-// workgroup per 32 x 32 output tile, its four waves on different k of the same tile. K advances in
-// 64-deep tiles of 8 groups of 8; wave w multiplies groups 2w and 2w + 1 (8 MFMAs per tile), so a
-// wave's MFMA chain is a quarter of K and the short grids spread over many more SIMDs. The four
-// partial sums meet in LDS, and wave w adds them up (in wave order) for rows 8w + 4*half + 0..3 of
-// the tile and runs the epilogue for those rows. Copies, swizzle and the clamped last k-tile as in
-// linear_mfma_kernel.
-template <int ACT, int EPI>
-__global__ __launch_bounds__(256) void linear_ksplit_kernel(LinearParams p, TileOrder order) {
-  constexpr int BM = 32, BN = 32, BK = 64, NS = 2;
-  constexpr int CPR = BK / 4;  // 16-byte chunks per tile row
-  constexpr int NG = BK / 8;   // groups of 8 k per tile, two per wave
+// Small products (under two 64 x 64 tiles per CU: the VAE projections, batch-2 DiT calls): one
+// workgroup per (32*TM) x (32*TN) output tile with KS waves on each of its 32 x 32 blocks, each of
+// them on different k (32 x 32 tiles with four splits, 32 x 64 tiles with two). K advances in 64-deep tiles of 8 groups of 8; the KS waves of a block
+// multiply 8/KS groups each, so a wave's MFMA chain is K/KS long and short grids spread over KS
+// times the waves. The partial sums meet in LDS, and the KS waves of a block add them up (in wave
+// order) for 16/KS of its accumulator registers each and run the epilogue for those rows. Copies,
+// swizzle and the clamped last k-tile as in linear_mfma_kernel.
+template <int TM, int TN, int KS, int ACT, int EPI>
+__global__ __launch_bounds__(64 * TM * TN * KS) void linear_ksplit_kernel(LinearParams p, TileOrder order) {
+  constexpr int BM = 32 * TM, BN = 32 * TN, BK = 64, NS = 2;
+  constexpr int NWAVE = TM * TN * KS;
+  constexpr int NT = 64 * NWAVE;     // threads
+  constexpr int CPR = BK / 4;        // 16-byte chunks per tile row
+  constexpr int NG = BK / 8;         // groups of 8 k per tile
+  constexpr int GPW = NG / KS;       // groups per wave
+  constexpr int RPW = 16 / KS;       // accumulator registers each wave finishes
   constexpr int A_TILE = BM * BK;
   constexpr int STAGE = (BM + BN) * BK;
-  constexpr int NI = BM * CPR / 256;  // DMA instructions per wave, tensor and stage
-  static_assert(NI * 256 == BM * CPR && BM == BN, "tiles must split into whole wave copies");
+  constexpr int NIA = BM * CPR / NT;  // DMA instructions per thread and stage
+  constexpr int NIB = BN * CPR / NT;
+  static_assert(NIA * NT == BM * CPR && NIB * NT == BN * CPR, "tiles must split into whole copies");
+  static_assert(GPW * KS == NG && RPW * KS == 16 && RPW % 4 == 0, "k split must divide the groups and rows");
+  static_assert(NWAVE * 16 * 64 <= NS * STAGE, "partial sums must fit in the tiles");
 
-  __shared__ __attribute__((aligned(16))) float lds[NS * STAGE];  // 32 KiB; the partial sums reuse it
+  __shared__ __attribute__((aligned(16))) float lds[NS * STAGE];  // the partial sums reuse it
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int blk = wave % (TM * TN);  // the wave's 32 x 32 block: rows 32*(blk / TN), columns 32*(blk % TN)
+  const int ks = wave / (TM * TN);   // its share of k
   const int col = lane & 31;
   const int half = lane >> 5;
 
@@ -369,17 +378,24 @@ __global__ __launch_bounds__(256) void linear_ksplit_kernel(LinearParams p, Tile
   const int mlast = min(BM, p.M - m0) - 1;
   const int nlast = min(BN, p.N - n0) - 1;
 
-  // chunk of DMA instruction n: physical chunk (n*4 + wave)*64 + lane, row pc / CPR, logical chunk
-  // c at physical c ^ (row % CPR)
-  unsigned aoff[NI], boff[NI];
-  int ccol[NI];
+  // chunk of DMA instruction n: physical chunk n*NT + tid, row pc / CPR, logical chunk c at
+  // physical c ^ (row % CPR)
+  unsigned aoff[NIA], boff[NIB];
+  int acol[NIA], bcol[NIB];
 #pragma unroll
-  for (int n = 0; n < NI; ++n) {
-    const int pc_all = (n * 4 + wave) * 64 + lane;
+  for (int n = 0; n < NIA; ++n) {
+    const int pc_all = n * NT + tid;
     const int row = pc_all / CPR;
     const int c = (pc_all % CPR) ^ (row % CPR);
-    ccol[n] = 4 * c;
+    acol[n] = 4 * c;
     aoff[n] = 4u * (unsigned)(min(row, mlast) * (int)p.ldx + 4 * c);
+  }
+#pragma unroll
+  for (int n = 0; n < NIB; ++n) {
+    const int pc_all = n * NT + tid;
+    const int row = pc_all / CPR;
+    const int c = (pc_all % CPR) ^ (row % CPR);
+    bcol[n] = 4 * c;
     boff[n] = 4u * (unsigned)(min(row, nlast) * (int)p.ldw + 4 * c);
   }
   const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(p.x + p.x_off + (int64_t)m0 * p.ldx);
@@ -390,40 +406,39 @@ __global__ __launch_bounds__(256) void linear_ksplit_kernel(LinearParams p, Tile
     constexpr int S = decltype(stage)::value;
     float* at = lds + S * STAGE;
     float* bt = at + A_TILE;
-    if (kt < nfull) {
-      const unsigned soff = 4u * (unsigned)(kt * BK);
+    // whole tiles copy at the k-tile's column; the tile holding K (always tile nfull) re-reads the
+    // last group for columns at or past K (never multiplied)
+    const bool last = kt >= nfull;
+    const int k0 = kt * BK;
+    const unsigned soff = 4u * (unsigned)k0;
+    const int kmax = p.K - 8 - k0;
 #pragma unroll
-      for (int n = 0; n < NI; ++n) {
-        buffer_to_lds16(xr, aoff[n], at + (n * 4 + wave) * 256, soff);
-        buffer_to_lds16(wr, boff[n], bt + (n * 4 + wave) * 256, soff);
-      }
-    } else {
-      // the tile holding K: columns at or past K re-read the last group (never multiplied)
-      const int k0 = nfull * BK;
-      const unsigned soff = 4u * (unsigned)k0;
-      const int kmax = p.K - 8 - k0;
+    for (int n = 0; n < NIA; ++n) {
+      const unsigned shift = last && acol[n] > kmax + 4 ? 4u * (unsigned)((acol[n] & ~7) - kmax) : 0u;
+      buffer_to_lds16(xr, aoff[n] - shift, at + (n * NWAVE + wave) * 256, soff);
+    }
 #pragma unroll
-      for (int n = 0; n < NI; ++n) {
-        const unsigned shift = 4u * (unsigned)(ccol[n] > kmax + 4 ? (ccol[n] & ~7) - kmax : 0);
-        buffer_to_lds16(xr, aoff[n] - shift, at + (n * 4 + wave) * 256, soff);
-        buffer_to_lds16(wr, boff[n] - shift, bt + (n * 4 + wave) * 256, soff);
-      }
+    for (int n = 0; n < NIB; ++n) {
+      const unsigned shift = last && bcol[n] > kmax + 4 ? 4u * (unsigned)((bcol[n] & ~7) - kmax) : 0u;
+      buffer_to_lds16(wr, boff[n] - shift, bt + (n * NWAVE + wave) * 256, soff);
     }
   };
 
   f32x16 acc = zero16();
   const int swz = col % CPR;
+  const int arow = 32 * (blk / TN) + col;  // the lane's A row and B row in the tile
+  const int brow = 32 * (blk % TN) + col;
   auto step = [&](int kt, auto stage) {
     constexpr int S = decltype(stage)::value;
     wait_vmcnt<0>();
     __syncthreads();  // tile kt is whole, and every wave is done with the stage the next copy fills
     if (kt + 1 < nkt) issue(kt + 1, std::integral_constant<int, S ^ 1>{});
     const int ng = kt < nfull ? NG : (p.K - nfull * BK) >> 3;  // valid groups of 8 k in this tile
-    const float* at = lds + S * STAGE + col * BK;
-    const float* bt = lds + S * STAGE + A_TILE + col * BK;
+    const float* at = lds + S * STAGE + arow * BK;
+    const float* bt = lds + S * STAGE + A_TILE + brow * BK;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int g = 2 * wave + u;
+    for (int u = 0; u < GPW; ++u) {
+      const int g = GPW * ks + u;
       if (g < ng) {
         const int c = 4 * ((2 * g + half) ^ swz);
         const f32x4 ra = *reinterpret_cast<const f32x4*>(at + c);
@@ -447,21 +462,22 @@ __global__ __launch_bounds__(256) void linear_ksplit_kernel(LinearParams p, Tile
 #pragma unroll
   for (int r = 0; r < 16; ++r) red[(wave * 16 + r) * 64 + lane] = acc[r];
   __syncthreads();
-  // ---- epilogue: wave w finishes registers 4w..4w+3 = rows 8w + 4*half + 0..3 of column n0 + col
-  const int n = n0 + col;
+  // ---- epilogue: the wave finishes registers RPW*ks .. of its block: register r holds row
+  // 8(r/4) + 4*half + r%4 of column col
+  const int n = n0 + 32 * (blk % TN) + col;
   if (n >= p.N) return;
   const float bias_n = p.bias ? p.bias[n] : 0.f;
   float gate_n = 1.f;
   if constexpr (EPI == LIN_EPI_RESID_GATE) gate_n = p.gate[p.gate_off + n];
   const float* rsrc = p.resid ? p.resid : p.y;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int r = 4 * wave + k;
-    const int m = m0 + 8 * wave + 4 * half + k;
+  for (int k = 0; k < RPW; ++k) {
+    const int r = RPW * ks + k;
+    const int m = m0 + 32 * (blk / TN) + 8 * (r >> 2) + 4 * half + (r & 3);
     if (m < p.M) {
-      float sum = red[r * 64 + lane];
+      float sum = red[(blk * 16 + r) * 64 + lane];
 #pragma unroll
-      for (int w = 1; w < 4; ++w) sum += red[(w * 16 + r) * 64 + lane];
+      for (int w = 1; w < KS; ++w) sum += red[((w * TM * TN + blk) * 16 + r) * 64 + lane];
       float v = apply_act<ACT>(fmaf(sum, p.alpha, bias_n));
       const int64_t e = p.y_off + (int64_t)m * p.ldy + n;
       if constexpr (EPI != LIN_EPI_STORE) v = fmaf(gate_n, v, rsrc[e]);
@@ -554,35 +570,37 @@ hipError_t launch_epi(const LinearParams& p, hipStream_t stream) {
   }
 }
 
-template <int ACT, int EPI>
+template <int TM, int TN, int KS, int ACT, int EPI>
 hipError_t launch_ksplit_tiles(const LinearParams& p, hipStream_t stream) {
   TileOrder o;
-  o.tiles_m = (p.M + 31) / 32;
-  o.tiles_n = (p.N + 31) / 32;
+  o.tiles_m = (p.M + 32 * TM - 1) / (32 * TM);
+  o.tiles_n = (p.N + 32 * TN - 1) / (32 * TN);
   o.group_n = o.tiles_n;  // the operands of these small products stay in the L2
   o.sb_rows = (o.tiles_m + 7) / 8;
   const int64_t n = (int64_t)o.tiles_m * o.tiles_n;
   if (n > 0x7fffffff) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((linear_ksplit_kernel<ACT, EPI>), dim3((unsigned)n), dim3(256), 0, stream, p, o);
+  hipLaunchKernelGGL((linear_ksplit_kernel<TM, TN, KS, ACT, EPI>), dim3((unsigned)n), dim3(64 * TM * TN * KS), 0, stream,
+                     p, o);
   return hipGetLastError();
 }
 
-template <int ACT>
+template <int TM, int TN, int KS, int ACT>
 hipError_t launch_ksplit_epi(const LinearParams& p, hipStream_t stream) {
   switch (p.epi) {
-    case LIN_EPI_STORE: return launch_ksplit_tiles<ACT, LIN_EPI_STORE>(p, stream);
-    case LIN_EPI_RESID: return launch_ksplit_tiles<ACT, LIN_EPI_RESID>(p, stream);
-    case LIN_EPI_RESID_GATE: return launch_ksplit_tiles<ACT, LIN_EPI_RESID_GATE>(p, stream);
+    case LIN_EPI_STORE: return launch_ksplit_tiles<TM, TN, KS, ACT, LIN_EPI_STORE>(p, stream);
+    case LIN_EPI_RESID: return launch_ksplit_tiles<TM, TN, KS, ACT, LIN_EPI_RESID>(p, stream);
+    case LIN_EPI_RESID_GATE: return launch_ksplit_tiles<TM, TN, KS, ACT, LIN_EPI_RESID_GATE>(p, stream);
     default: return hipErrorInvalidValue;
   }
 }
 
+template <int TM, int TN, int KS>
 hipError_t launch_ksplit(const LinearParams& p, hipStream_t stream) {
   switch (p.act) {
-    case LIN_ACT_NONE: return launch_ksplit_epi<LIN_ACT_NONE>(p, stream);
-    case LIN_ACT_GELU: return launch_ksplit_epi<LIN_ACT_GELU>(p, stream);
-    case LIN_ACT_GELU_TANH: return launch_ksplit_epi<LIN_ACT_GELU_TANH>(p, stream);
-    case LIN_ACT_SILU: return launch_ksplit_epi<LIN_ACT_SILU>(p, stream);
+    case LIN_ACT_NONE: return launch_ksplit_epi<TM, TN, KS, LIN_ACT_NONE>(p, stream);
+    case LIN_ACT_GELU: return launch_ksplit_epi<TM, TN, KS, LIN_ACT_GELU>(p, stream);
+    case LIN_ACT_GELU_TANH: return launch_ksplit_epi<TM, TN, KS, LIN_ACT_GELU_TANH>(p, stream);
+    case LIN_ACT_SILU: return launch_ksplit_epi<TM, TN, KS, LIN_ACT_SILU>(p, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -619,21 +637,26 @@ LinearTile linear_mfma_tile(const LinearParams& p, int num_cus) {
   // per CU take linear_ksplit_kernel, whose quarter-K waves spread them over the SIMDs (us, 64 x 64
   // -> k-split: VAE output projection 1024 x 512 x 512 11.75 -> 8.1, context k|v 77 x 1152 x 576 13.2
   // -> 6.3, batch-2 proj/q/cproj 512 x 576 x 576 12.6-13.0 -> 8.4-8.7, fc1 512 x 2304 x 576 21.4 ->
-  // 19.2, fc2 512 x 576 x 2304 43.4 -> 23.0); wider grids keep 64 x 64 tiles, whose operands are
-  // shared by twice the outputs (VAE q|k|v 1024 x 1536 x 512, 384 tiles: 18.7 against 18.9-19.4).
+  // 19.2, fc2 512 x 576 x 2304 43.4 -> 23.0). Grids of 1.25 to 2 such tiles per CU take 32 x 64
+  // tiles with k split in two, whose count is twice that and so shares out more evenly over the CUs
+  // (VAE q|k|v 1024 x 1536 x 512, 384 tiles: 64 x 64 18.7-19.2, 32 x 64 / two splits 17.4, 64 x 32
+  // 17.5, 64 x 32 / four splits 17.9, 64 x 64 / two splits 20.7, 32 x 32 / four splits 18.9-19.4);
+  // wider grids keep 64 x 64 tiles.
   const int64_t tiles_wide = ((p.M + 127) / 128) * ((p.N + 191) / 192);
   const int64_t tiles_tall = ((p.M + 63) / 64) * ((p.N + 191) / 192);
   const int64_t tiles_64 = ((p.M + 63) / 64) * ((p.N + 63) / 64);
   if (p.N >= 2048 && tiles_wide >= num_cus) return {2, 3, 32, 2, 0};
   if ((p.N % 192 == 0 || p.N >= 1024) && tiles_tall >= 3 * (int64_t)num_cus) return {1, 3, 16, 3, 0};
-  if (4 * tiles_64 < 5 * (int64_t)num_cus) return {1, 1, 64, 2, 1};
+  if (4 * tiles_64 < 5 * (int64_t)num_cus) return {1, 1, 64, 2, 4};
+  if (tiles_64 < 2 * (int64_t)num_cus) return {1, 2, 64, 2, 2};
   return {1, 1, 32, 2, 0};
 }
 
 const char* linear_kernel_name(const LinearParams& p, int num_cus) {
   if (!linear_mfma_supported(p)) return "linear_generic";
   const LinearTile t = linear_mfma_tile(p, num_cus);
-  if (t.ksplit) return "linear_mfma_32x32_ksplit";
+  if (t.ksplit == 4) return "linear_mfma_32x32_ksplit";
+  if (t.ksplit == 2) return "linear_mfma_32x64_ksplit";
   if (t.wm == 2) return "linear_mfma_128x192";
   if (t.wn == 3) return "linear_mfma_64x192";
   return "linear_mfma_64x64";
@@ -647,7 +670,8 @@ hipError_t launch_linear(const LinearParams& p, int num_cus, hipStream_t stream)
     return hipGetLastError();
   }
   const LinearTile t = linear_mfma_tile(p, num_cus);
-  if (t.ksplit) return launch_ksplit(p, stream);
+  if (t.ksplit == 4) return launch_ksplit<1, 1, 4>(p, stream);
+  if (t.ksplit == 2) return launch_ksplit<1, 2, 2>(p, stream);
   if (t.wm == 2) return launch_act<2, 3, 32, 2>(p, stream);
   if (t.wn == 3) return launch_act<1, 3, 16, 3>(p, stream);
   return launch_act<1, 1, 32, 2>(p, stream);

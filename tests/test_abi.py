@@ -388,7 +388,8 @@ def lin_args(**over):
 
 def test_linear_kernel_choice():
     # DiT layers at batch 64 (16384 rows): 64 x 192 or 128 x 192 tiles while the grid fills the chip; grids of fewer
-    # 64 x 64 tiles than 1.25 per CU: 32 x 32 tiles with the k split over the workgroup's waves; else 64 x 64
+    # 64 x 64 tiles than 1.25 per CU: 32 x 32 tiles with the k split over the workgroup's waves; under 2 per CU:
+    # 32 x 64 tiles, k split in two; else 64 x 64
     assert _lib.linear_kernel_name(lin_args(M=16384, N=1728, K=576)) == "linear_mfma_64x192"       # qkv
     assert _lib.linear_kernel_name(lin_args(M=16384, N=2304, K=576)) == "linear_mfma_128x192"      # fc1
     assert _lib.linear_kernel_name(lin_args(M=16384, N=576, K=576)) == "linear_mfma_64x192"        # proj, q, cproj
@@ -398,7 +399,8 @@ def test_linear_kernel_choice():
     assert _lib.linear_kernel_name(lin_args(M=1024, N=512, K=512)) == "linear_mfma_32x32_ksplit"   # VAE output
     assert _lib.linear_kernel_name(lin_args(M=4096, N=600, K=576)) == "linear_mfma_64x64"
     assert _lib.linear_kernel_name(lin_args(M=77, N=1152, K=576)) == "linear_mfma_32x32_ksplit"  # small call
-    assert _lib.linear_kernel_name(lin_args(M=1024, N=1536, K=512)) == "linear_mfma_64x64"  # VAE q|k|v
+    assert _lib.linear_kernel_name(lin_args(M=1024, N=1536, K=512)) == "linear_mfma_32x64_ksplit"  # VAE q|k|v
+    assert _lib.linear_kernel_name(lin_args(M=2000, N=1024, K=512)) == "linear_mfma_64x64"  # 512 tiles
     assert _lib.linear_kernel_name(lin_args(K=36)) == "linear_generic"            # K % 8 != 0
     assert _lib.linear_kernel_name(lin_args(x_off=1)) == "linear_generic"         # unaligned rows
     assert _lib.linear_kernel_name(lin_args(x=FAKE + 4)) == "linear_generic"

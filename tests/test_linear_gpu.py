@@ -100,12 +100,17 @@ def test_large_tiles_ragged(dev, M, N, K, tile):
     (250, 97, 568, _lib.SA_EPI_RESID, _lib.SA_ACT_SILU, "32x32_ksplit"),
     (1000, 512, 2304, _lib.SA_EPI_STORE, _lib.SA_ACT_GELU, "32x32_ksplit"),  # long K (288 MFMAs per wave)
     (33, 1152, 64, _lib.SA_EPI_STORE, _lib.SA_ACT_NONE, "32x32_ksplit"),     # one whole k-tile
-    # 64 x 64 tiles (more than 1.25 tiles per CU, too few for the larger tiles), ragged
-    (2000, 700, 200, _lib.SA_EPI_RESID_GATE, _lib.SA_ACT_NONE, "64x64"),
+    # k-split 32 x 64 tiles (1.25 to 2 64 x 64 tiles per CU): ragged; N = 970 leaves the last tile's second
+    # 32-column block wholly past N; K = 136 is two k-tiles and one group of 8
+    (2000, 700, 200, _lib.SA_EPI_RESID_GATE, _lib.SA_ACT_NONE, "32x64_ksplit"),
+    (1500, 970, 136, _lib.SA_EPI_RESID, _lib.SA_ACT_SILU, "32x64_ksplit"),
+    (1024, 1536, 512, _lib.SA_EPI_STORE, _lib.SA_ACT_NONE, "32x64_ksplit"),  # VAE q|k|v
+    # 64 x 64 tiles (two tiles per CU and more, too few for the larger tiles), ragged
+    (3000, 700, 200, _lib.SA_EPI_RESID_GATE, _lib.SA_ACT_NONE, "64x64"),
 ])
 def test_small_grid_tiles(dev, M, N, K, epi, act, tile):
-    """The two small-grid tiles: the k-split kernel (the four waves of a workgroup on different k of one
-    32 x 32 tile, partial sums added in LDS, each wave storing a quarter of the rows) and the 64 x 64 tile."""
+    """The small-grid tiles: the k-split kernel (the waves of a workgroup on different k of one 32 x 32 or
+    32 x 64 tile, partial sums added in LDS, each wave storing its share of the rows) and the 64 x 64 tile."""
     call = make_linear(f"small_{M}x{N}x{K}", M, N, K, seed=M + 3 * N + K, act=act, epi=epi,
                        gate_off=5 if epi == _lib.SA_EPI_RESID_GATE else 0)
     run_checked(dev, call, expect_kernel=f"linear_mfma_{tile}")
