@@ -367,13 +367,26 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
       // The D/32 output tiles are independent accumulation chains: interleaving them (each P
       // register feeding one MFMA per tile in turn) keeps the MFMA pipe fed while an exp2 or an
       // LDS read is still in flight.
+      auto pv_group = [&](auto g) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
+        for (int r = 4 * g; r < 4 * g + 4; ++r) {
 #pragma unroll
-        for (int t = 0; t < NDB; ++t) {
-          const float vv = vPrefetch ? vpre[r * NDB + t] : vrow[32 * (t ^ half) + (8 * (r >> 2) + (r & 3)) * D];
-          oacc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, pr[r], oacc[t], 0, 0, 0);
+          for (int t = 0; t < NDB; ++t) {
+            const float vv = vPrefetch ? vpre[r * NDB + t] : vrow[32 * (t ^ half) + (8 * (r >> 2) + (r & 3)) * D];
+            oacc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, pr[r], oacc[t], 0, 0, 0);
+          }
         }
+      };
+      // Key-length masks: in the block holding the last valid key, P registers 8..15 (keys 16..31)
+      // are all zero when at most 16 keys are valid, and V rows there are finite copies of the last
+      // valid key, so their products are skipped with every sum bitwise the same (sweep
+      // cross-attention 35.0 -> 34.0 us; skipping by groups of 8 keys, three branches, 34.6 us)
+      constexpr bool kSkip = MASK == MASK_KEY_LEN || MASK == MASK_KEY_LEN_ORDERED;
+      pv_group(std::integral_constant<int, 0>{});
+      pv_group(std::integral_constant<int, 1>{});
+      if (!kSkip || kv_len - k0 > 16) {
+        pv_group(std::integral_constant<int, 2>{});
+        pv_group(std::integral_constant<int, 3>{});
       }
     }
   };
