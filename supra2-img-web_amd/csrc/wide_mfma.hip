@@ -2,9 +2,9 @@
 // (app/models/vae.js:86: one head, D = C = 512, 1024 tokens), which the reference sends down its
 // unfused GEMM -> softmax -> GEMM path (app/gpu/ops.js:119-147).
 //
-// Work decomposition
-//   One workgroup = NW wave64s = 32 queries x one chunk of keys (NW = 8 for D = 512: two waves per
-//   SIMD; 4 for D = 256). Wave w owns the head-dim slice [w*D/NW, (w+1)*D/NW) of Q, K, V and O:
+// Work decomposition (wide_mfma_kernel, D = 256; D = 512 runs wide_rows_kernel, described there)
+//   One workgroup = NW = 4 wave64s = 32 queries x one chunk of keys. Wave w owns the head-dim
+//   slice [w*D/NW, (w+1)*D/NW) of Q, K, V and O:
 //   per 32-key block it computes the partial score tile S_w^T = K_w Q_w^T over its slice
 //   (v_mfma_f32_32x32x2f32, the same transposed layout as the flash kernel), the NW partial tiles
 //   are summed through LDS in two stages in a fixed order (so every wave derives bit-identical
@@ -17,9 +17,11 @@
 //   rescale (the kernel boundary orders the two; no atomics or cross-XCD fences).
 //
 // LDS per workgroup: K and V slices [32 keys][D/NW] per wave (XOR-swizzled as in the flash kernel)
-// plus the score exchange: 160 KiB for D = 512 (one workgroup per CU), 80 KiB for D = 256.
+// plus the score exchange: 80 KiB for D = 256 (two workgroups per CU).
 
 #include <algorithm>
+#include <type_traits>
+#include <utility>
 
 #include "common.h"
 #include "kernels.h"
@@ -30,6 +32,15 @@ namespace {
 
 constexpr float kRescaleSlack = 8.f;
 
+// f(std::integral_constant<int, 0>{}) ... f(std::integral_constant<int, N - 1>{}), in order
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;
@@ -291,6 +302,283 @@ __global__ __launch_bounds__(64 * NW, 1) void wide_mfma_kernel(AttnParams p, int
   }
 }
 
+// D = 512: one workgroup = 4 waves = 32 queries x one chunk of keys, taken in rounds of four
+// 32-key blocks. In a round wave w computes the whole score tile of block w over all 512 head
+// dims (256 MFMAs in two independent chains: K rows straight from memory into registers, Q^T from
+// a copy of the query tile in LDS), the four block maxima and row sums meet in LDS (one reference
+// m per query for the round, so the probabilities need no lazy rescale inside it), each wave
+// publishes its probabilities, and wave w then accumulates O^T for its quarter of the head dims
+// over all four blocks (V rows straight into registers, prefetched a block ahead, with head dim
+// 4i + t of the quarter on row i of output tile t, so one 16-byte load feeds the four tiles).
+// Each probability is computed once per round, where the head-dim-split kernel above summed
+// partial score tiles through LDS and took the softmax in every wave for every block; one wave
+// per SIMD, its loads software-pipelined. Writes the same partial records as wide_mfma_kernel
+// (merged by wide_merge_kernel), staged through LDS into whole-row stores.
+template <int MASK>
+__global__ __launch_bounds__(256, 1) void wide_rows_kernel(AttnParams p, int q_groups, int nks, int chunk, float* ws) {
+  constexpr int D = 512;
+  constexpr int NG = D / 8;          // groups of 8 head dims (4 MFMAs) per score tile
+  constexpr int DS = D / 4;          // output head dims per wave
+  constexpr int REC = 32 * D + 64;   // workspace floats per partial: O [32][D], m [32], l [32]
+  constexpr int KR = 8;              // K groups in flight ahead of the MFMAs (16 measured no faster)
+  constexpr int NQ = 32 * D / 4 / 256;  // 16-byte Q chunks per thread
+
+  __shared__ __attribute__((aligned(16))) float lds_q[32 * D];      // [quarter][query][128], then the output
+  __shared__ __attribute__((aligned(16))) f32x4 lds_p[4 * 4 * 64];  // [block][r/4][lane]
+  __shared__ float lds_m[4 * 32];                                   // [block][query]
+  __shared__ float lds_l[4 * 32];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31;
+  const int half = lane >> 5;
+
+  int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int kc = tile % nks;
+  tile /= nks;
+  const int g = tile % q_groups;
+  tile /= q_groups;
+  const int h = tile % p.H;
+  const int b = tile / p.H;
+  const int q0 = g * 32;
+  const int slot_base = ((b * p.H + h) * q_groups + g) * nks;
+
+  int kv_len = p.Lk;
+  if constexpr (MASK == MASK_KEY_LEN) kv_len = min(max(p.key_len[b], 0), p.Lk);
+  const int kbeg = kc * chunk;
+  const int kend = min(kbeg + chunk, kv_len);
+  const int rounds = kend > kbeg ? (kend - kbeg + 127) >> 7 : 0;
+
+  const float* kbase = p.k + p.k_off + (int64_t)b * p.sk + h * D;
+  const float* vbase = p.v + p.v_off + (int64_t)b * p.sv + h * D + wave * DS;
+
+  // ---- Q tile (rows past Lq re-read the last row) into registers, then into LDS a quarter of 128
+  // head dims at a time as the score products reach it: [quarter][query][32 chunks of 16 bytes],
+  // chunk c of row r at c ^ (r & 15). Thread t holds physical chunks n*256 + t (n = 0..15), so
+  // quarter k is its registers 4k..4k+3. (Copies straight into LDS would make the compiler wait
+  // for all of them, and the K loads behind them, before the first LDS read.)
+  f32x4 qst[NQ];
+  {
+    const float* qbase = p.q + p.q_off + (int64_t)b * p.sq + h * D;
+#pragma unroll
+    for (int n = 0; n < NQ; ++n) {
+      const int pc = (n & 3) * 256 + tid;  // physical chunk within quarter n / 4
+      const int row = pc >> 5;
+      const int c = 32 * (n >> 2) + ((pc & 31) ^ (row & 15));
+      qst[n] = *reinterpret_cast<const f32x4*>(qbase + (int64_t)min(q0 + row, p.Lq - 1) * p.ldq + 4 * c);
+    }
+  }
+
+  // V rows of one block for this wave's head dims: register r holds V[key][4*col .. 4*col + 3] of
+  // key 8(r/4) + 4*half + r%4 of the block. The buffer ends after the chunk's last valid key, so
+  // rows past it read as zeros (their probabilities are zero) and no load needs a branch: a
+  // conditional load is sunk by the compiler to its first use, which would undo the prefetch.
+  unsigned vrow_off[16];  // byte offset of register r's row and columns from the block's first row
+#pragma unroll
+  for (int r = 0; r < 16; ++r) vrow_off[r] = 4u * (unsigned)((4 * half + 8 * (r >> 2) + (r & 3)) * (int)p.ldv + 4 * col);
+  auto load_v = [&](int kb0, f32x4* dst) {
+    // (in a scalar register: a clamp the compiler computes on the vector unit would make the
+    // descriptor look divergent and every load a waterfall loop)
+    const int rows = __builtin_amdgcn_readfirstlane(max(0, min(32, kend - kb0)));
+    const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(vbase + (int64_t)kb0 * p.ldv), 0, rows * (int)p.ldv * 4, 0x00020000);
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      dst[r] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, vrow_off[r], 0, 0));
+  };
+
+  f32x16 oacc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) oacc[t] = zero16();
+  float m = kMaxSeed;
+  float l = 0.f;
+  // the swizzled Q chunk 2i + half of this lane's query (quarter i / 16)
+  const float* qrow = lds_q + col * 128;
+
+  for (int rd = 0; rd < rounds; ++rd) {
+    const int rb0 = kbeg + 128 * rd;  // first key of the round
+    if (rd > 0) __syncthreads();      // every wave is done with the previous round's exchange
+    const int kb0 = rb0 + 32 * wave;  // this wave's score block
+    const bool has_keys = kb0 < kend;  // false for the missing blocks of a short last round
+    // K rows of the block (clamped past the chunk's last key), 16 bytes per group of 8 dims
+    const __amdgpu_buffer_rsrc_t kr = buffer_rsrc(kbase + (int64_t)kb0 * p.ldk);
+    const unsigned koff = 4u * (unsigned)((min(kb0 + col, kend - 1) - kb0) * (int)p.ldk + 4 * half);
+    auto load_k = [&](int i) {
+      return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff + 32u * i, 0, 0));
+    };
+    f32x4 kring[KR];
+    if (has_keys) {
+#pragma unroll
+      for (int i = 0; i < KR; ++i) kring[i] = load_k(i);
+    }
+    // round 0 publishes the Q quarters as the products reach them
+    auto q_quarter = [&](auto k) {
+      constexpr int kq = decltype(k)::value;
+      if (rd == 0) {
+#pragma unroll
+        for (int n = 4 * kq; n < 4 * kq + 4; ++n) *reinterpret_cast<f32x4*>(lds_q + n * 1024 + 4 * tid) = qst[n];
+        __syncthreads();
+      }
+    };
+    q_quarter(std::integral_constant<int, 0>{});
+    f32x4 vbuf[2][16];  // V of the round's blocks, double-buffered
+    float u[16];
+    if (has_keys) {
+      f32x16 sa = zero16(), sb = zero16();
+      auto read_q = [&](int i) {
+        return *reinterpret_cast<const f32x4*>(qrow + (i >> 4) * 4096 + 4 * ((2 * (i & 15) + half) ^ (col & 15)));
+      };
+      // Groups in pairs, group i into sa and i + 1 into sb (the compiler orders the products; pinning
+      // them to alternate between the chains measured the same). The Q operands of the next pair
+      // are read during this one.
+      f32x4 qn0 = read_q(0), qn1 = read_q(1);
+      static_for<NG / 2>([&](auto I) {
+        constexpr int i = 2 * decltype(I)::value;
+        const f32x4 k0v = kring[i % KR], k1v = kring[(i + 1) % KR];
+        const f32x4 q0v = qn0, q1v = qn1;
+        if constexpr (i + KR < NG) {
+          kring[i % KR] = load_k(i + KR);
+          kring[(i + 1) % KR] = load_k(i + 1 + KR);
+        }
+        if constexpr (i == NG - 16) load_v(rb0, vbuf[0]);  // the round's first V block streams in under the last products
+        if constexpr (i + 2 < NG) {
+          if constexpr ((i + 2) % 16 == 0) q_quarter(std::integral_constant<int, (i + 2) / 16>{});
+          qn0 = read_q(i + 2);
+          qn1 = read_q(i + 3);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          sa = __builtin_amdgcn_mfma_f32_32x32x2f32(k0v[j], q0v[j], sa, 0, 0, 0);
+          sb = __builtin_amdgcn_mfma_f32_32x32x2f32(k1v[j], q1v[j], sb, 0, 0, 0);
+        }
+        // keeps each load where it is issued: left free, the scheduler sinks the ring's loads to
+        // just before their use, one group ahead of the products
+        __builtin_amdgcn_sched_barrier(0);
+      });
+#pragma unroll
+      for (int r = 0; r < 16; ++r) u[r] = (sa[r] + sb[r]) * p.scale_log2;
+      if (kb0 + 32 > kend) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kb0 + 8 * (r >> 2) + 4 * half + (r & 3);
+          u[r] = key < kend ? u[r] : -INFINITY;
+        }
+      }
+    } else {
+      // the score-less wave still takes part in round 0's quarter barriers
+      q_quarter(std::integral_constant<int, 1>{});
+      q_quarter(std::integral_constant<int, 2>{});
+      q_quarter(std::integral_constant<int, 3>{});
+      load_v(rb0, vbuf[0]);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) u[r] = -INFINITY;
+    }
+    // ---- one reference per query for the round: the maximum over the four blocks
+    float mb = u[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) mb = max_nan(mb, u[r]);
+    mb = max_with_partner(mb);
+    if (half == 0) lds_m[wave * 32 + col] = mb;
+    __syncthreads();
+    float m_new = max_nan(m, lds_m[col]);
+    m_new = max_nan(m_new, lds_m[32 + col]);
+    m_new = max_nan(m_new, lds_m[64 + col]);
+    m_new = max_nan(m_new, lds_m[96 + col]);
+    if (rd > 0) {
+      const float alpha = fast_exp2(m - m_new);
+      l *= alpha;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) oacc[t] *= alpha;
+    }
+    m = m_new;
+    float ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      u[r] = fast_exp2(u[r] - m);
+      ps += u[r];
+    }
+    ps = sum_with_partner(ps);
+    if (half == 0) lds_l[wave * 32 + col] = ps;
+#pragma unroll
+    for (int k4 = 0; k4 < 4; ++k4) {
+      f32x4 x;
+      x[0] = u[4 * k4 + 0];
+      x[1] = u[4 * k4 + 1];
+      x[2] = u[4 * k4 + 2];
+      x[3] = u[4 * k4 + 3];
+      lds_p[(wave * 4 + k4) * 64 + lane] = x;
+    }
+    __syncthreads();
+    l += lds_l[col] + lds_l[32 + col] + lds_l[64 + col] + lds_l[96 + col];
+    // ---- O^T += V^T P^T over the round's blocks, this wave's 128 head dims; the next block's V
+    // is requested before this block's products (a zero-row buffer past the keys: no access)
+    float pr[4][16];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int k4 = 0; k4 < 4; ++k4) {
+        const f32x4 x = lds_p[(j * 4 + k4) * 64 + lane];
+        pr[j][4 * k4 + 0] = x[0];
+        pr[j][4 * k4 + 1] = x[1];
+        pr[j][4 * k4 + 2] = x[2];
+        pr[j][4 * k4 + 3] = x[3];
+      }
+    static_for<4>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      if constexpr (j + 1 < 4) load_v(rb0 + 32 * (j + 1), vbuf[(j + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (rb0 + 32 * j < kend) {  // wave-uniform: blocks past the chunk's keys hold no probabilities
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            oacc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(vbuf[j & 1][r][t], pr[j][r], oacc[t], 0, 0, 0);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  }
+
+  // ---- output: O^T tile t, register r holds head dim wave*128 + 4i + t of query col, with
+  // i = 8(r/4) + 4*half + r%4, so the four tiles' register r are four consecutive head dims.
+  // The wave stages its 32 x 128 slice in LDS (the Q tile is dead: every wave has passed the
+  // last exchange, after its score products), 16-byte chunk i of query q at i ^ q, and stores
+  // it back as 512-byte row pieces, two rows per instruction, instead of 16 bytes of 32 rows.
+  const float inv = nks == 1 ? (l > 0.f ? 1.f / l : 0.f) : 1.f;
+  float* stage = lds_q + wave * 32 * DS;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int i = 8 * (r >> 2) + 4 * half + (r & 3);
+    f32x4 x;
+    x[0] = oacc[0][r] * inv;
+    x[1] = oacc[1][r] * inv;
+    x[2] = oacc[2][r] * inv;
+    x[3] = oacc[3][r] * inv;
+    *reinterpret_cast<f32x4*>(stage + col * DS + 4 * (i ^ col)) = x;
+  }
+  float* dst;
+  int64_t ld;
+  if (nks == 1) {
+    dst = p.o + p.o_off + (int64_t)b * p.so + (int64_t)q0 * p.ldo + h * D + wave * DS;
+    ld = p.ldo;
+  } else {
+    float* rec = ws + (int64_t)(slot_base + kc) * REC;
+    dst = rec + wave * DS;
+    ld = D;
+    if (wave == 0 && half == 0) {
+      rec[32 * D + col] = m;
+      rec[32 * D + 32 + col] = l;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int row = 2 * j + half;  // query q0 + row; lane col holds chunk col of it
+    const f32x4 x = *reinterpret_cast<const f32x4*>(stage + row * DS + 4 * (col ^ row));
+    if (nks > 1 || q0 + row < p.Lq) *reinterpret_cast<f32x4*>(dst + (int64_t)row * ld + 4 * col) = x;
+  }
+}
+
 // Combines the nks partial records of every query group: one thread per (query, 4 dims),
 // O = sum_c O_c exp2(m_c - m) / sum_c l_c exp2(m_c - m) with m = max_c m_c (0 if every l_c is 0).
 template <int D>
@@ -359,10 +647,11 @@ __global__ __launch_bounds__(256) void wide_merge_kernel(AttnParams p, int q_gro
   *reinterpret_cast<f32x4*>(p.o + p.o_off + (int64_t)b * p.so + (int64_t)qi * p.ldo + h * D + 4 * d4) = y;
 }
 
-// Waves per workgroup: each owns D / NW head dims. D = 512 runs 8 waves (two per SIMD, 160 KiB of
-// LDS), D = 256 runs 4 (80 KiB, two workgroups per CU).
+// Waves per workgroup of the head-dim-split kernel (D = 256): each owns D / 4 head dims, 80 KiB of
+// LDS, two workgroups per CU. (At D = 512 it ran 8 waves, two per SIMD, in 160 KiB: VAE call
+// 34.9 us against 29.9 for wide_rows_kernel.)
 template <int D>
-constexpr int kWideWaves = D == 512 ? 8 : 4;
+constexpr int kWideWaves = 4;
 
 template <int D>
 hipError_t launch_d(const AttnParams& p, const WidePlan& plan, float* ws, hipStream_t stream) {
@@ -370,7 +659,14 @@ hipError_t launch_d(const AttnParams& p, const WidePlan& plan, float* ws, hipStr
   const int64_t n = (int64_t)p.B * p.H * plan.q_groups * plan.nks;
   if (n > 0x7fffffff) return hipErrorInvalidConfiguration;
   const dim3 grid((unsigned)n), block(64 * NW);
-  if (p.mask_mode == MASK_KEY_LEN)
+  if constexpr (D == 512) {
+    if (p.mask_mode == MASK_KEY_LEN)
+      hipLaunchKernelGGL((wide_rows_kernel<MASK_KEY_LEN>), grid, dim3(256), 0, stream, p, plan.q_groups, plan.nks,
+                         plan.chunk, ws);
+    else
+      hipLaunchKernelGGL((wide_rows_kernel<MASK_NONE>), grid, dim3(256), 0, stream, p, plan.q_groups, plan.nks,
+                         plan.chunk, ws);
+  } else if (p.mask_mode == MASK_KEY_LEN)
     hipLaunchKernelGGL((wide_mfma_kernel<D, NW, MASK_KEY_LEN>), grid, block, 0, stream, p, plan.q_groups, plan.nks,
                        plan.chunk, ws);
   else
@@ -396,13 +692,16 @@ WidePlan wide_mfma_plan(const AttnParams& p, int num_cus) {
   WidePlan plan;
   plan.q_groups = (p.Lq + 31) / 32;
   const int64_t base = (int64_t)p.B * p.H * plan.q_groups;
-  const int per_cu = p.D == 512 ? 1 : 2;  // LDS: 144 KiB (D=512) or 80 KiB (D=256) per workgroup
+  // one workgroup per CU at D = 512 (one wave per SIMD at 400 registers), two at D = 256 (80 KiB LDS)
+  const int per_cu = p.D == 512 ? 1 : 2;
   const int64_t target = (int64_t)num_cus * per_cu;
   const int nblk = (p.Lk + 31) / 32;
   int nks = 1;
   if (base < target) nks = (int)((target + base - 1) / base);
   nks = std::max(1, std::min({nks, nblk, kWideMaxChunks}));
-  const int blocks_per_chunk = (nblk + nks - 1) / nks;
+  // D = 512 takes keys in rounds of four blocks (wide_rows_kernel): chunks of whole rounds
+  const int unit = p.D == 512 ? 4 : 1;
+  const int blocks_per_chunk = (nblk + nks * unit - 1) / (nks * unit) * unit;
   plan.chunk = 32 * blocks_per_chunk;
   plan.nks = (p.Lk + plan.chunk - 1) / plan.chunk;  // chunks that hold at least one key
   plan.ws_floats = plan.nks > 1 ? base * plan.nks * (int64_t)(32 * p.D + 64) : 0;

@@ -158,7 +158,11 @@ def test_generic_head_dims(dev, D):
 
 
 @pytest.mark.parametrize("D,B,H,Lq,Lk", [(512, 1, 1, 1024, 1024), (512, 1, 1, 33, 300), (256, 2, 3, 70, 200),
-                                          (512, 2, 2, 64, 40), (256, 1, 1, 1, 1)])
+                                          (512, 2, 2, 64, 40), (256, 1, 1, 1, 1),
+                                          # D = 512 in several rounds of four key blocks per workgroup: one
+                                          # chunk per query group (3 rounds, the last with one wave's block
+                                          # and a partial one), and 10 chunks of 2 rounds, the last chunk short
+                                          (512, 8, 1, 1024, 300), (512, 1, 1, 64, 2500)])
 def test_wide_shapes(dev, D, B, H, Lq, Lk):
     call = make_call(B=B, H=H, D=D, Lq=Lq, Lk=Lk, seed=D + Lq + Lk)
     assert _lib.kernel_name(Staged(dev, call).args) == f"wide_mfma_d{D}"
@@ -190,6 +194,19 @@ def test_wide_key_len_and_workspace_reuse(dev):
     assert e["finite"] and e["rel_l2"] <= TOL and e["max_rel"] <= TOL, e
     s2.release()
     st.release()
+
+
+def test_wide_rounds_with_key_lengths(dev):
+    """D = 512, one key chunk per query group (256 query groups fill the chip), so each workgroup takes
+    its keys in rounds of four blocks with the reference moved between rounds; key lengths leave
+    0, 1, 2 or 3 rounds, whole blocks and single keys."""
+    lens = [0, 1, 31, 32, 33, 127, 128, 129, 200, 255, 256, 257, 299, 300, 64, 96]
+    call = make_call(B=16, H=1, D=512, Lq=512, Lk=300, mask_mode=_lib.SA_MASK_KEY_LEN, key_len=lens, seed=21)
+    st = Staged(dev, call)
+    assert st.kernel == "wide_mfma_d512"
+    assert _lib.plan(st.args).key_chunks == 1
+    st.release()
+    run_checked(dev, call, check_fp64=False)
 
 
 def test_wide_large_batch_without_key_split(dev):
