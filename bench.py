@@ -671,7 +671,25 @@ def main() -> int:
     value = step_flops * args.steps / (total_ms * 1e-3) / 1e12
     log(f"sweep: {ms_per_step:.3f} ms/step, {value:.2f} TFLOP/s")
 
-    # per-launch timing of each kernel over the same sweep (separate instrumented pass)
+    # Per-launch time of each kernel: the sweep's self-attention calls back to back (the 14 input
+    # sets in turn, one event pair over steps x 14 calls), then its cross-attention calls likewise.
+    # Launch gaps are included; no event sits between launches.
+    def b2b(idx: int) -> float:
+        for pair in staged:
+            pair[idx].launch()
+        a, z = Event(), Event()
+        a.record(dev.stream)
+        for _ in range(args.steps):
+            for pair in staged:
+                pair[idx].launch()
+        z.record(dev.stream)
+        dev.sync()
+        return a.elapsed_ms(z) / (args.steps * data.blocks)
+
+    self_ms = b2b(0)
+    cross_ms = b2b(1)
+    # the same with an event pair around every launch inside the sweep's alternation (each pair adds
+    # its own record overhead to the launch it brackets)
     pairs_s = [(Event(), Event()) for _ in range(args.steps * data.blocks)]
     pairs_c = [(Event(), Event()) for _ in range(args.steps * data.blocks)]
     n = 0
@@ -687,13 +705,14 @@ def main() -> int:
             b.record(dev.stream)
             n += 1
     dev.sync()
-    self_ms = sum(a.elapsed_ms(b) for a, b in pairs_s) / len(pairs_s)
-    cross_ms = sum(a.elapsed_ms(b) for a, b in pairs_c) / len(pairs_c)
+    self_ms_ev = sum(a.elapsed_ms(b) for a, b in pairs_s) / len(pairs_s)
+    cross_ms_ev = sum(a.elapsed_ms(b) for a, b in pairs_c) / len(pairs_c)
     self_call = staged[0][0].call
     self_flops = self_call.flops()
     achieved = self_flops / (self_ms * 1e-3) / 1e12
     cross_flops = sum(c.call.flops() for _, c in staged) / len(staged)
-    log(f"per launch: self {self_ms * 1e3:.1f} us ({achieved:.1f} TFLOP/s), cross {cross_ms * 1e3:.1f} us")
+    log(f"per launch: self {self_ms * 1e3:.1f} us ({achieved:.1f} TFLOP/s), cross {cross_ms * 1e3:.1f} us "
+        f"(one event pair per launch: {self_ms_ev * 1e3:.1f} / {cross_ms_ev * 1e3:.1f} us)")
 
     # caller side: per-sample launches (the reference's loops) against the batched call sites
     callsite = callsite_block(dev, staged[0][0], staged[0][1])
@@ -784,7 +803,10 @@ def main() -> int:
             "algorithmic_flops_per_launch": self_flops,
             "algorithmic_bytes_per_launch": self_call.algorithmic_bytes(),
             "us_per_launch": round(self_ms * 1e3, 3),
+            "us_per_launch_timing": "back to back, one event pair over steps x 14 launches",
+            "us_per_launch_event_pair_each": round(self_ms_ev * 1e3, 3),
             "cross_us_per_launch": round(cross_ms * 1e3, 3),
+            "cross_us_per_launch_event_pair_each": round(cross_ms_ev * 1e3, 3),
             "cross_tflops": round(cross_flops / (cross_ms * 1e-3) / 1e12, 3),
         },
         "per_config": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
