@@ -10,6 +10,7 @@
 #include <math.h>
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 #include <stddef.h>
 #include <stdarg.h>
 #include <stdint.h>
@@ -91,12 +92,71 @@ bool too_large(int64_t v) { return v >= kMaxExtent; }
 // Size of the revision-2 struct (it ended at workspace_bytes); still accepted.
 constexpr uint32_t kAttnArgsV2Size = offsetof(sa_attn_args, key_len_host);
 
-// Longest-first schedule for per-sequence key lengths known on the host: sequences sorted by key
-// blocks, longest first (stable), then dealt round-robin over the 8 L2 domains when B is a
-// multiple of 8. The flash grid's workgroup remap gives domain x the sequence ranks
-// [x*B/8, (x+1)*B/8) in launch order, so every domain gets an even share of the long sequences and
-// starts its own longest first; the short ones fill the tail. Allocation-free (B <= kMaxOrder).
-void longest_first(const int32_t* len, int B, int Lk, uint8_t* order) {
+int num_cus();
+
+// Schedule for per-sequence key lengths known on the host (order[rank] = sequence). The flash
+// grid's workgroup remap gives L2 domain (XCD) x the ranks [x*B/8, (x+1)*B/8) in launch order, T
+// consecutive units (query tiles x heads) per rank, and within a domain the hardware deals
+// workgroup j of the first residency to CU j % C (C CUs per domain, four workgroups per CU; the
+// later workgroups take the first slots that free up). A CU's time is about the sum of its units'
+// key blocks, so:
+//   1. sequences sorted by key blocks, longest first (stable), go to the domain with the least work
+//      so far among those not yet full (B/8 each) - the sums per domain come out nearly equal;
+//   2. in each domain, from longest first, pairs of positions are swapped while that lowers the
+//      heaviest CU's blocks (then the sum of squares) in a simulation of that dealing.
+// The model puts the heaviest CU of the batch-64 sweep's cross-attention at 12 blocks (the bound)
+// against 13 for dealing longest first round-robin; on the hardware, where later workgroups take
+// whichever slot frees first, some CUs still get 13. Measured against the round-robin deal: 34.3 ->
+// 33.8 us for the launch, 120.1 -> 118.6 us for a self + cross pair; step 1 alone measured 34.5 us.
+// The search is bounded (kSearchOps simulated workgroup placements; a miss measured 0.5-1.2 ms of
+// host time at batch 64; the sweep's cross-attention converges in two passes, 0.24M): a launch too large for one pass
+// over the pairs takes the round-robin deal of the longest-first order, and a B that 8 does not
+// divide plain longest first. The result depends on the key lengths only and is cached for the
+// last kScheduleSlots length sets (the DiT runs every block and step with the same prompts, and a
+// classifier-free-guidance caller alternates two sets).
+constexpr int64_t kSearchOps = 1 << 19;
+constexpr int kScheduleSlots = 4;
+
+struct ScheduleSlot {
+  int B = 0, Lk = 0, C = 0;
+  int64_t T = 0;
+  int32_t len[sa::kMaxOrder];
+  uint8_t order[sa::kMaxOrder];
+};
+struct ScheduleCache {
+  std::mutex mu;
+  int next = 0;  // slot the next miss replaces
+  ScheduleSlot slot[kScheduleSlots];
+};
+ScheduleCache g_schedule;
+
+int64_t simulate_domain(const uint8_t* seq, int n, const int* nb, int T, int C, int64_t* sumsq) {
+  int load[64];
+  for (int c = 0; c < C; ++c) load[c] = 0;
+  int j = 0;
+  for (int r = 0; r < n; ++r) {
+    const int w = nb[seq[r]];
+    for (int t = 0; t < T; ++t, ++j) {
+      if (j < 4 * C) {
+        load[j % C] += w;
+      } else {  // a later workgroup: the slot that frees first, taken as the least loaded CU
+        int best = 0;
+        for (int c = 1; c < C; ++c)
+          if (load[c] < load[best]) best = c;
+        load[best] += w;
+      }
+    }
+  }
+  int64_t mx = 0, sq = 0;
+  for (int c = 0; c < C; ++c) {
+    mx = std::max<int64_t>(mx, load[c]);
+    sq += (int64_t)load[c] * load[c];
+  }
+  *sumsq = sq;
+  return mx;
+}
+
+void balanced_schedule(const int32_t* len, int B, int Lk, int64_t T, int C, uint8_t* order) {
   int idx[sa::kMaxOrder], nb[sa::kMaxOrder];
   for (int i = 0; i < B; ++i) {
     nb[i] = (std::min(std::max(len[i], 0), Lk) + 31) / 32;
@@ -104,10 +164,73 @@ void longest_first(const int32_t* len, int B, int Lk, uint8_t* order) {
     for (; j > 0 && nb[idx[j - 1]] < nb[i]; --j) idx[j] = idx[j - 1];  // insertion sort, stable
     idx[j] = i;
   }
-  for (int j = 0; j < B; ++j) {
-    const int rank = B % 8 == 0 ? (j % 8) * (B / 8) + j / 8 : j;
-    order[rank] = (uint8_t)idx[j];
+  if (B % 8 != 0) {
+    for (int j = 0; j < B; ++j) order[j] = (uint8_t)idx[j];
+    return;
   }
+  const int per = B / 8;
+  // Work of one simulation (workgroups, the later ones scanning C CUs) and of one pass over the
+  // pairs of every domain; without room for one pass, the round-robin deal.
+  const int64_t units = per * std::min<int64_t>(std::max<int64_t>(T, 1), 1 << 20);
+  const int64_t sim_ops = units + std::max<int64_t>(units - 4 * C, 0) * C;
+  const int64_t pairs = (int64_t)per * (per - 1) / 2;
+  if (pairs == 0 || C < 1 || C > 64 || T < 1 || T > (1 << 20) || 8 * pairs * sim_ops > kSearchOps) {
+    for (int j = 0; j < B; ++j) order[(j % 8) * per + j / 8] = (uint8_t)idx[j];
+    return;
+  }
+  int64_t total[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int count[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int j = 0; j < B; ++j) {
+    int best = -1;
+    for (int x = 0; x < 8; ++x)
+      if (count[x] < per && (best < 0 || total[x] < total[best])) best = x;
+    order[best * per + count[best]++] = (uint8_t)idx[j];
+    total[best] += nb[idx[j]];
+  }
+  const int64_t domain_ops = kSearchOps / 8;
+  for (int x = 0; x < 8; ++x) {
+    uint8_t* seq = order + x * per;  // longest first within the domain already
+    int64_t sq, spent = sim_ops;
+    int64_t mx = simulate_domain(seq, per, nb, (int)T, C, &sq);
+    bool improved = true;
+    for (int pass = 0; pass < 8 && improved; ++pass) {
+      improved = false;
+      for (int u = 0; u < per; ++u)
+        for (int v = u + 1; v < per && spent + sim_ops <= domain_ops; ++v) {
+          if (nb[seq[u]] == nb[seq[v]]) continue;
+          std::swap(seq[u], seq[v]);
+          int64_t sq2;
+          const int64_t mx2 = simulate_domain(seq, per, nb, (int)T, C, &sq2);
+          spent += sim_ops;
+          if (mx2 < mx || (mx2 == mx && sq2 < sq)) {
+            mx = mx2;
+            sq = sq2;
+            improved = true;
+          } else {
+            std::swap(seq[u], seq[v]);
+          }
+        }
+    }
+  }
+}
+
+void cached_schedule(const int32_t* len, int B, int Lk, int64_t T, int C, uint8_t* order) {
+  std::lock_guard<std::mutex> lock(g_schedule.mu);
+  for (const ScheduleSlot& s : g_schedule.slot)
+    if (s.B == B && s.Lk == Lk && s.T == T && s.C == C &&
+        memcmp(s.len, len, (size_t)B * sizeof(int32_t)) == 0) {
+      memcpy(order, s.order, (size_t)B);
+      return;
+    }
+  balanced_schedule(len, B, Lk, T, C, order);
+  ScheduleSlot& s = g_schedule.slot[g_schedule.next];
+  g_schedule.next = (g_schedule.next + 1) % kScheduleSlots;
+  s.B = B;
+  s.Lk = Lk;
+  s.T = T;
+  s.C = C;
+  memcpy(s.len, len, (size_t)B * sizeof(int32_t));
+  memcpy(s.order, order, (size_t)B);
 }
 
 // Resolves an sa_attn_args into kernel parameters; returns SA_OK or an error (message set).
@@ -238,7 +361,9 @@ int resolve(const sa_attn_args* a, sa::AttnParams* p) {
   // launch order already.
   p->order_n = 0;
   if (a->mask_mode == SA_MASK_KEY_LEN && key_len_host && a->B >= 8 && a->B <= sa::kMaxOrder) {
-    longest_first(key_len_host, a->B, a->Lk, p->order);
+    // units per sequence of the 128-query flash grid the schedule is made for
+    cached_schedule(key_len_host, a->B, a->Lk, (int64_t)a->H * ((a->Lq + 127) / 128), num_cus() / 8,
+                    p->order);
     for (int r = 0; r < a->B; ++r)
       if (p->order[r] != r) {
         p->order_n = a->B;

@@ -1,12 +1,13 @@
-"""The longest-first sequence schedule (sa_attn_args.key_len_host, GPU).
+"""The balanced sequence schedule (sa_attn_args.key_len_host, GPU).
 
-A host copy of the per-sequence key lengths lets the library launch the longest sequences first,
-balanced over the L2 domains. It changes only which workgroup runs which sequence, so the output
+A host copy of the per-sequence key lengths lets the library order the sequences so that the L2
+domains and their CUs get even shares of key blocks (longest first, balanced over the domains, then a
+bounded swap search per domain). It changes only which workgroup runs which sequence, so the output
 must be bit-identical with the host copy, without it, and with a stale (wrong) host copy - the
 kernel reads the device key lengths for the arithmetic - and must match the oracle at the usual
-bar. Cases: the sweep's batch-64 cross-attention (round-robin over the domains), batch 24 (also a
-multiple of 8), batch 13 (plain longest-first order) and batch 2 (below the batch the schedule is
-used for, so all three runs take the launch order)."""
+bar. Cases: the sweep's batch-64 cross-attention (searched), batch 24 (also a multiple of 8), batch
+128 with two query tiles (16 sequences per domain), batch 13 (plain longest-first order) and batch 2
+(below the batch the schedule is used for, so all three runs take the launch order)."""
 
 from __future__ import annotations
 
@@ -25,11 +26,11 @@ TOL = 1e-5
 
 def _calls():
     yield "sweep_cross_b64", workloads.SweepData(blocks=1).block(0)[1]
-    for B, seed in ((24, 31), (13, 32), (2, 33)):
+    for B, H, Lq, seed in ((24, 9, 256, 31), (128, 2, 128, 34), (13, 9, 256, 32), (2, 9, 256, 33)):
         rng = np.random.default_rng(seed)
         key_len = [int(x) for x in rng.integers(0, 129, size=B)]  # zero-length sequences included
         key_len[0] = 128
-        yield f"B{B}", make_call(B=B, H=9, D=64, Lq=256, Lk=128, seed=seed, mask_mode=_lib.SA_MASK_KEY_LEN,
+        yield f"B{B}", make_call(B=B, H=H, D=64, Lq=Lq, Lk=128, seed=seed, mask_mode=_lib.SA_MASK_KEY_LEN,
                                  key_len=key_len)
 
 
