@@ -6,7 +6,8 @@ bounded swap search per domain). It changes only which workgroup runs which sequ
 must be bit-identical with the host copy, without it, and with a stale (wrong) host copy - the
 kernel reads the device key lengths for the arithmetic - and must match the oracle at the usual
 bar. Cases: the sweep's batch-64 cross-attention (searched), batch 24 (also a multiple of 8), batch
-128 with two query tiles (16 sequences per domain), batch 13 (plain longest-first order) and batch 2
+128 with two query tiles (16 sequences per domain), batch 58 with ragged queries (1044 units over
+unequal L2 domains, plain longest-first order), batch 13 (plain longest-first order) and batch 2
 (below the batch the schedule is used for, so all three runs take the launch order)."""
 
 from __future__ import annotations
@@ -26,7 +27,7 @@ TOL = 1e-5
 
 def _calls():
     yield "sweep_cross_b64", workloads.SweepData(blocks=1).block(0)[1]
-    for B, H, Lq, seed in ((24, 9, 256, 31), (128, 2, 128, 34), (13, 9, 256, 32), (2, 9, 256, 33)):
+    for B, H, Lq, seed in ((24, 9, 256, 31), (128, 2, 128, 34), (58, 9, 250, 35), (13, 9, 256, 32), (2, 9, 256, 33)):
         rng = np.random.default_rng(seed)
         key_len = [int(x) for x in rng.integers(0, 129, size=B)]  # zero-length sequences included
         key_len[0] = 128
@@ -39,7 +40,7 @@ CALLS = list(_calls())
 
 @pytest.mark.parametrize("name,call", CALLS, ids=[c[0] for c in CALLS])
 def test_schedule_is_bitwise_neutral(dev, name, call):
-    print(f"[schedule case] {name} B={call.B} kernel=", end="", flush=True)
+    print(f"[schedule case] {name} B={call.B} Lq={call.Lq} kernel=", end="", flush=True)
     outs = {}
     for mode in ("host", "none", "stale"):
         st = Staged(dev, call, out_fill=np.nan, host_key_len=mode != "none")
