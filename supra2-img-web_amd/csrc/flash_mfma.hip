@@ -165,11 +165,12 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
     koff[n] = 4u * (unsigned)(row * (int)p.ldk + ck);
     voff[n] = 4u * (unsigned)(row * (int)p.ldv + cv);
   }
-  auto issue = [&](int step, int buf) {
+  // rows past `lim` (the key length, or Lk for a speculative issue) re-read row lim - 1
+  auto issue = [&](int step, int buf, int lim) {
     float* kt = lds + buf * 2 * TILE;
     float* vt = kt + TILE;
     const int key0 = step * KT;
-    if (key0 + KT <= kv_len) {
+    if (key0 + KT <= lim) {
       const __amdgpu_buffer_rsrc_t kr = buffer_rsrc(kbase + (int64_t)key0 * p.ldk);
       const __amdgpu_buffer_rsrc_t vr = buffer_rsrc(vbase + (int64_t)key0 * p.ldv);
 #pragma unroll
@@ -184,7 +185,7 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
         const int blk64 = n * 4 + wave;
         int row, ck, cv;
         chunk_of(n, row, ck, cv);
-        const int key = min(key0 + row, kv_len - 1);
+        const int key = min(key0 + row, lim - 1);
         load_to_lds16(kbase + (int64_t)key * p.ldk + ck, kt + blk64 * 256);
         load_to_lds16(vbase + (int64_t)key * p.ldv + cv, vt + blk64 * 256);
       }
@@ -229,7 +230,16 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
       }
     }
   }
-  if (nstep > 0) issue(0, 0);  // the first tile streams in while Q loads
+  // Key-length launches of the single-split kernels issue their first two tiles before the key
+  // length is known (rows past Lk clamped): one dependent load less before the first data. Keys past
+  // the length are masked out of the scores, and the V rows past it, which may hold anything, are
+  // zeroed in LDS before the products that read them (spec_fix below).
+  constexpr bool kSpec = (MASK == MASK_KEY_LEN || MASK == MASK_KEY_LEN_ORDERED) && NSPLIT == 1;
+  if constexpr (kSpec) {
+    if (p.Lk > 0) issue(0, 0, p.Lk);
+  } else if (nstep > 0) {
+    issue(0, 0, kv_len);  // the first tile streams in while Q loads
+  }
 
   // ---- Q into registers, pre-scaled: lane holds scale*log2(e)*Q[qi][8i + 4*half + j] in qr[4i + j]
   float qr[QREG];
@@ -242,7 +252,11 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
     // Stage 1 is unused until the loop: the second step's tile streams in from the start too,
     // rather than after the first barrier (which left the two-step loops of the key-split
     // kernels waiting for their second tile).
-    if (nstep > 1) issue(1, 1);
+    if constexpr (kSpec) {
+      if (p.Lk > KT) issue(1, 1, p.Lk);
+    } else if (nstep > 1) {
+      issue(1, 1, kv_len);
+    }
     if constexpr (MASK == MASK_KEY_LEN_ORDERED) __builtin_amdgcn_s_setprio(0);
 #pragma unroll
     for (int i = 0; i < QREG / 4; ++i) {
@@ -265,12 +279,23 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
     // step 1 itself was issued before the loop) overwrites
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (step >= 1 && step + 1 < nstep) issue(step + 1, buf ^ 1);
+    if (step >= 1 && step + 1 < nstep) issue(step + 1, buf ^ 1, kv_len);
     const int blk = step * NSPLIT + ks;
     if (blk < nblk) {
       const int k0 = blk * 32;
       const float* kt = lds + buf * 2 * TILE;
       const float* vt = kt + TILE;
+      // a speculatively issued tile holding the last valid key: its V rows past the key length are
+      // zeroed (every thread its own chunks, rows pc / CPR) before the PV products read them
+      const bool spec_fix = kSpec && step <= 1 && k0 + 32 > kv_len;
+      if (spec_fix) {
+        float* vw = lds + buf * 2 * TILE + TILE;
+#pragma unroll
+        for (int i = 0; i < KT * CPR / 256; ++i) {
+          const int pc = tid + 256 * i;
+          if (k0 + pc / CPR >= kv_len) *reinterpret_cast<f32x4*>(vw + 4 * pc) = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
       // ---- u^T = K (scaled Q)^T for 32 keys x 32 queries
       f32x16 s = zero16();
       const float* krow = kt + (ks * 32 + col) * D;
@@ -382,6 +407,7 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
       // valid key, so their products are skipped with every sum bitwise the same (sweep
       // cross-attention 35.0 -> 34.0 us; skipping by groups of 8 keys, three branches, 34.6 us)
       constexpr bool kSkip = MASK == MASK_KEY_LEN || MASK == MASK_KEY_LEN_ORDERED;
+      if (spec_fix) __syncthreads();  // the zeroed V rows are in place
       pv_group(std::integral_constant<int, 0>{});
       pv_group(std::integral_constant<int, 1>{});
       if (!kSkip || kv_len - k0 > 16) {
@@ -444,6 +470,8 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
   if constexpr (NSPLIT == 1) {
     // through LDS: each wave writes its 32 x D tile (16-byte chunks swizzled by row, conflict-free
     // both ways) and reads it back as whole rows, CPR lanes per row
+    // speculative tiles the loop never waited for (zero or one step) have landed before LDS is reused
+    if constexpr (kSpec) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();  // every wave is done with the K/V tiles
     float* ot = lds + wave * 32 * D;
 #pragma unroll

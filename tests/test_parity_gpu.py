@@ -113,6 +113,47 @@ def test_key_len_including_zero(dev):
     run_checked(dev, call)
 
 
+PADDING_CASES = [
+    # (B, H, D, Lq, Lk, host copy of the lengths): the 4-per-CU flash kernel with and without the
+    # schedule, the small-launch kernel, head dim 128, and the wide kernels
+    (64, 9, 64, 256, 128, True),
+    (64, 9, 64, 256, 128, False),
+    (6, 2, 64, 64, 128, False),
+    (32, 8, 128, 256, 160, True),
+    (2, 1, 512, 96, 300, False),
+    (2, 2, 256, 64, 200, False),
+]
+
+
+@pytest.mark.parametrize("B,H,D,Lq,Lk,host", PADDING_CASES, ids=[f"B{c[0]}D{c[2]}k{c[4]}{'h' if c[5] else ''}"
+                                                                 for c in PADDING_CASES])
+def test_key_len_padding_is_never_used(dev, B, H, D, Lq, Lk, host):
+    """Keys past a sequence's length may hold anything (the reference runs each sample at its own
+    Lk, app/models/dit.js:182-185): with NaN and Inf in every K and V row past the length, the output
+    equals the attention over the valid keys alone (the oracle on the original, finite inputs)."""
+    rng = np.random.default_rng(B * 1000 + D + Lk)
+    key_len = rng.integers(0, Lk + 1, size=B).astype(np.int32)
+    key_len[: min(B, 5)] = [0, 1, 31, 33, Lk][: min(B, 5)]
+    call = make_call(B=B, H=H, D=D, Lq=Lq, Lk=Lk, mask_mode=_lib.SA_MASK_KEY_LEN, key_len=key_len, seed=B + D)
+    ref = orc.reference_torch(call)
+    ld = call.args["ldk"]
+    k = call.k.reshape(B, Lk, ld).copy()
+    v = call.v.reshape(B, Lk, ld).copy()
+    for b in range(B):
+        k[b, key_len[b]:] = np.nan
+        v[b, key_len[b]:] = np.where(np.arange(ld) % 2 == 0, np.inf, np.nan).astype(np.float32)
+    call.k, call.v = k.reshape(-1), v.reshape(-1)
+    print(f"[case] padding B={B} H={H} D={D} Lq={Lq} Lk={Lk} host={host}", flush=True)
+    st = Staged(dev, call, out_fill=SENTINEL, host_key_len=host)
+    try:
+        print(f"  kernel {st.kernel}", flush=True)
+        out = st.run()
+    finally:
+        st.release()
+    e = orc.errors(orc.output_view(out, call), ref)
+    assert e["finite"] and e["rel_l2"] <= TOL and e["max_rel"] <= TOL, e
+
+
 def test_key_mask_random_and_empty(dev):
     call = make_call(B=3, H=2, D=64, Lq=50, Lk=100, mask_mode=_lib.SA_MASK_KEY_MASK, seed=5)
     call.key_mask[1, :] = 0  # a sequence with no attended key -> zeros
