@@ -104,7 +104,7 @@ typedef struct sa_attn_args {
   void* workspace;                    /* device scratch, 16-byte aligned, when the call needs it */
   int64_t workspace_bytes;            /* its size (>= sa_attention_workspace_bytes(args)) */
   /* Revision 3. KEY_LEN: an optional HOST copy of key_len[0..B), read during the call and used
-   * only to schedule the sequences longest first (balanced over the device's L2 domains) when
+   * only to schedule the sequences (balanced by key blocks over the device's L2 domains and CUs) when
    * 8 <= B <= 256; the results come from the device key_len either way, so a stale copy costs
    * speed, never correctness. The DiT caller knows its prompt lengths on the host
    * (app/models/dit.js:137-144). */
@@ -153,7 +153,7 @@ const char* sa_attention_kernel_name(const sa_attn_args* args);
 #define SA_KERNEL_GENERIC 3 /* generic_kernel (any head dim <= 1024, any alignment) */
 #define SA_KERNEL_FLASH_SMALL 4 /* flash_small_kernel<key_split waves, bias_mode, mask_variant>: head dim 64,
                                    one workgroup per 32 queries, for launches of at most 256 such groups */
-/* mask_variant beyond the SA_MASK_* values: per-sequence key lengths plus the longest-first
+/* mask_variant beyond the SA_MASK_* values: per-sequence key lengths plus the host
  * sequence schedule (SA_MASK_KEY_LEN with key_len_host, 8 <= B <= 256, order not the identity) */
 #define SA_MASK_VARIANT_KEY_LEN_SCHEDULED 3
 

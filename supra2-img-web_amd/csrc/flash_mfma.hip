@@ -83,7 +83,8 @@ constexpr int kMinBlocksPerCU = (D == 64 && NSPLIT == 1 && BIAS == BIAS_NONE && 
 // memory system takes to deliver the first tiles of one workgroup per CU over the whole chip.
 constexpr unsigned kStaggerTicks = 350;
 
-// The longest-first sequence schedule: a second kernel argument of the scheduled variant only.
+// The host sequence schedule (order[rank] = sequence): a second kernel argument of the scheduled
+// variant only.
 struct FlashOrder {
   uint8_t order[kMaxOrder];
 };
@@ -131,7 +132,7 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
   tile /= q_tiles;
   const int h = tile % p.H;
   int b = tile / p.H;
-  if constexpr (MASK == MASK_KEY_LEN_ORDERED) b = ord.order[b];  // the longest-first schedule
+  if constexpr (MASK == MASK_KEY_LEN_ORDERED) b = ord.order[b];  // the host schedule
   const int q0 = qtile * QT;
   const int qi = q0 + qg * 32 + col;
   const bool q_valid = qi < p.Lq;

@@ -13,8 +13,8 @@
 //                      which folds the per-sample loops of dit.js:170-185 into one call;
 //   ldo                output row stride (default H*D, as ops.js:114);
 //   keyLen             Tensor int32 [B]: keys j >= keyLen[b] are masked (padded cross-attention);
-//   keyLenHost         optional Int32Array copy of keyLen on the host: the library then schedules
-//                      the sequences longest first (results come from keyLen either way);
+//   keyLenHost         optional Int32Array copy of keyLen on the host: the library then balances
+//                      the sequences over the CUs (results come from keyLen either way);
 //   keyMask, smask     Tensor uint8 [B, smask]: nonzero = attend (SDPA boolean convention);
 //   relpos             { table: Tensor f32 [numBuckets, H], lut: Tensor i32 [Lq + Lk - 1] }: the
 //                      T5 relative-position bias gathered in-kernel instead of a dense bias;

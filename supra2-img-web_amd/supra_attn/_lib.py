@@ -153,7 +153,7 @@ class AttnArgs(ctypes.Structure):
         ("smask", c_int64),
         ("workspace", c_void_p),
         ("workspace_bytes", c_int64),
-        ("key_len_host", c_void_p),  # revision 3: host copy of key_len, schedules longest first
+        ("key_len_host", c_void_p),  # revision 3: host copy of key_len, for the sequence schedule
     ]
 
     def __init__(self, **kw):

@@ -13,7 +13,7 @@ class Staged:
     """Device-resident buffers of one call plus its ready-to-launch sa_attn_args.
 
     With per-sequence key lengths, the host copy of the lengths goes along too (key_len_host), so
-    the library schedules the sequences longest first, as the DiT caller does; host_key_len=False
+    the library schedules the sequences (balanced by key blocks), as the DiT caller does; host_key_len=False
     leaves it out (the launch-order schedule)."""
 
     def __init__(self, dev: Device, call: Call, out_fill: float | None = None, host_key_len: bool = True):

@@ -34,7 +34,7 @@ BIAS_NAMES = {0: "none", 1: "dense", 2: "relpos"}
 
 def key_lengths(rng, B: int, Lk: int, split: int) -> np.ndarray:
     """Mostly long sequences (two steps or more per splitting wave), plus a ragged short one, a
-    zero and a full one; not sorted, so the longest-first schedule is not the identity."""
+    zero and a full one; not sorted, so the sequence schedule is not the identity."""
     lo = 32 * (2 * split - 1) + 1  # last splitting wave still gets two blocks
     kl = rng.integers(min(lo, Lk), Lk + 1, size=B).astype(np.int32)
     kl[1] = Lk
