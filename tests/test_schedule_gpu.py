@@ -58,3 +58,30 @@ def test_schedule_is_bitwise_neutral(dev, name, call):
     ref = orc.reference_torch(call)
     e = orc.errors(orc.output_view(outs["host"], call), ref)
     assert e["finite"] and e["rel_l2"] <= TOL and e["max_rel"] <= TOL, e
+
+
+RANDOM_BATCHES = [8, 16, 40, 72, 96, 200, 256]
+
+
+@pytest.mark.parametrize("B", RANDOM_BATCHES)
+def test_schedule_random_batches(dev, B):
+    """The schedule over batch sizes that exercise every path of its construction (18 units of 128
+    queries per sequence): one sequence per L2 domain (B = 8, no swaps), the bounded swap search
+    (16-72), a search too large for its budget (the round-robin deal of the longest-first order,
+    96-256), with random lengths including zero and full ones: bit-identical to the launch-order run
+    and within the usual bar of the oracle."""
+    rng = np.random.default_rng(100 + B)
+    key_len = rng.integers(0, 129, size=B).astype(np.int32)
+    key_len[0], key_len[-1] = 0, 128
+    call = make_call(B=B, H=9, D=64, Lq=256, Lk=128, seed=B, mask_mode=_lib.SA_MASK_KEY_LEN, key_len=key_len)
+    print(f"[schedule random] B={B}", flush=True)
+    outs = {}
+    for mode in ("host", "none"):
+        st = Staged(dev, call, out_fill=np.nan, host_key_len=mode == "host")
+        try:
+            outs[mode] = st.run()
+        finally:
+            st.release()
+    np.testing.assert_array_equal(outs["none"].view(np.uint32), outs["host"].view(np.uint32))
+    e = orc.errors(orc.output_view(outs["host"], call), orc.reference_torch(call))
+    assert e["finite"] and e["rel_l2"] <= TOL and e["max_rel"] <= TOL, e
