@@ -177,10 +177,18 @@ typedef struct sa_attn_plan {
   int32_t tail_kernel;
   int32_t tail_key_split;
   int64_t tail_workgroups;
+  /* Revision 2 (appended: a revision-1 struct, which ends at tail_workgroups, is still accepted and
+   * these fields are then not written). The host sequence schedule of a FLASH call whose
+   * mask_variant is SA_MASK_VARIANT_KEY_LEN_SCHEDULED: sequence_order[r] is the sequence launched at
+   * rank r (r < B; when 8 divides B, L2 domain x takes the ranks [x*B/8, (x+1)*B/8)) and order_n is
+   * B; otherwise order_n is 0 and sequence_order all zero. */
+  int32_t order_n;
+  uint8_t sequence_order[256];
 } sa_attn_plan;
 
 /* Fills *plan for these arguments: SA_OK, or the status sa_attention_f32 would return for a
- * rejected call (nothing is launched either way). Host only. */
+ * rejected call (nothing is launched either way). plan->struct_size: sizeof(sa_attn_plan), or the
+ * revision-1 size (offsetof(sa_attn_plan, order_n)). Host only. */
 int sa_attention_plan(const sa_attn_args* args, sa_attn_plan* plan);
 
 /* Number of compiled kernel variants; sa_attention_variant(i, plan) describes variant i

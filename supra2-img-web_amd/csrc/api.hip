@@ -91,6 +91,8 @@ bool too_large(int64_t v) { return v >= kMaxExtent; }
 
 // Size of the revision-2 struct (it ended at workspace_bytes); still accepted.
 constexpr uint32_t kAttnArgsV2Size = offsetof(sa_attn_args, key_len_host);
+// Size of the revision-1 sa_attn_plan (it ended at tail_workgroups); still accepted.
+constexpr uint32_t kPlanV1Size = offsetof(sa_attn_plan, order_n);
 
 int num_cus();
 
@@ -164,7 +166,7 @@ void balanced_schedule(const int32_t* len, int B, int Lk, int64_t T, int C, uint
     for (; j > 0 && nb[idx[j - 1]] < nb[i]; --j) idx[j] = idx[j - 1];  // insertion sort, stable
     idx[j] = i;
   }
-  if (B % 8 != 0) {
+  if (B % 8 != 0 || nb[idx[0]] == nb[idx[B - 1]]) {  // (all equal: the launch order, i.e. no schedule)
     for (int j = 0; j < B; ++j) order[j] = (uint8_t)idx[j];
     return;
   }
@@ -725,8 +727,9 @@ const char* sa_attention_kernel_name(const sa_attn_args* args) {
 
 int sa_attention_plan(const sa_attn_args* args, sa_attn_plan* plan) {
   if (plan == nullptr) return fail(SA_ERR_INVALID, "plan is NULL");
-  if (plan->struct_size != sizeof(sa_attn_plan))
-    return fail(SA_ERR_INVALID, "plan struct_size %u does not match sizeof(sa_attn_plan) = %zu", plan->struct_size,
+  const uint32_t size = plan->struct_size;
+  if (size != sizeof(sa_attn_plan) && size != kPlanV1Size)
+    return fail(SA_ERR_INVALID, "plan struct_size %u does not match sizeof(sa_attn_plan) = %zu", size,
                 sizeof(sa_attn_plan));
   sa::AttnParams p;
   int rc = resolve(args, &p);
@@ -734,8 +737,11 @@ int sa_attention_plan(const sa_attn_args* args, sa_attn_plan* plan) {
   Choice c;
   rc = choose(p, &c);
   if (rc != SA_OK) return rc;
-  *plan = sa_attn_plan{};
-  plan->struct_size = sizeof(sa_attn_plan);
+  // filled in full here, then copied out up to the caller's struct_size
+  sa_attn_plan full{};
+  sa_attn_plan* const out = plan;
+  plan = &full;
+  plan->struct_size = size;
   plan->name = c.name;
   plan->bias_mode = p.bias_mode;
   plan->mask_variant = p.mask_mode;
@@ -773,6 +779,11 @@ int sa_attention_plan(const sa_attn_args* args, sa_attn_plan* plan) {
     plan->head_dim = p.D;
     plan->workgroups = (int64_t)p.B * p.H * p.Lq;
   }
+  if (plan->kernel == SA_KERNEL_FLASH && plan->mask_variant == SA_MASK_VARIANT_KEY_LEN_SCHEDULED) {
+    plan->order_n = p.B;
+    memcpy(plan->sequence_order, p.order, (size_t)p.B);
+  }
+  memcpy(out, plan, size);
   return ok();
 }
 
@@ -784,15 +795,19 @@ int32_t sa_attention_variant_count(void) {
 
 int sa_attention_variant(int32_t index, sa_attn_plan* plan) {
   if (plan == nullptr) return fail(SA_ERR_INVALID, "plan is NULL");
-  if (plan->struct_size != sizeof(sa_attn_plan))
-    return fail(SA_ERR_INVALID, "plan struct_size %u does not match sizeof(sa_attn_plan) = %zu", plan->struct_size,
+  const uint32_t size = plan->struct_size;
+  if (size != sizeof(sa_attn_plan) && size != kPlanV1Size)
+    return fail(SA_ERR_INVALID, "plan struct_size %u does not match sizeof(sa_attn_plan) = %zu", size,
                 sizeof(sa_attn_plan));
   const int nflash = sa::flash_mfma_variants(nullptr, 0);
   const int nsmall = sa::flash_small_variants(nullptr, 0);
   if (index < 0 || index >= sa_attention_variant_count())
     return fail(SA_ERR_INVALID, "variant index %d outside [0, %d)", index, sa_attention_variant_count());
-  *plan = sa_attn_plan{};
-  plan->struct_size = sizeof(sa_attn_plan);
+  // filled in full here, then copied out up to the caller's struct_size
+  sa_attn_plan full{};
+  sa_attn_plan* const out = plan;
+  plan = &full;
+  plan->struct_size = size;
   if (index >= nflash && index < nflash + nsmall) {
     sa::FlashVariant v[64];
     if (sa::flash_small_variants(v, 64) > 64) return fail(SA_ERR_UNSUPPORTED, "variant table overflow");
@@ -803,6 +818,7 @@ int sa_attention_variant(int32_t index, sa_attn_plan* plan) {
     plan->bias_mode = x.bias;
     plan->mask_variant = x.mask;
     plan->name = sa::flash_small_name(x.nsplit);
+    memcpy(out, plan, size);
     return ok();
   }
   if (index >= nflash) index -= nsmall;
@@ -827,6 +843,7 @@ int sa_attention_variant(int32_t index, sa_attn_plan* plan) {
     plan->kernel = SA_KERNEL_GENERIC;
     plan->name = "generic";
   }
+  memcpy(out, plan, size);
   return ok();
 }
 

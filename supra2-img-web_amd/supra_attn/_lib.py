@@ -181,6 +181,8 @@ class AttnPlan(ctypes.Structure):
         ("tail_kernel", c_int32),
         ("tail_key_split", c_int32),
         ("tail_workgroups", c_int64),
+        ("order_n", c_int32),  # revision 2: the host sequence schedule of a scheduled flash call
+        ("sequence_order", ctypes.c_uint8 * 256),
     ]
 
     def __init__(self):
