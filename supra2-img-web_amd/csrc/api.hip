@@ -99,9 +99,9 @@ int num_cus();
 // Schedule for per-sequence key lengths known on the host (order[rank] = sequence). The flash
 // grid's workgroup remap gives L2 domain (XCD) x the ranks [x*B/8, (x+1)*B/8) in launch order, T
 // consecutive units (query tiles x heads) per rank, and within a domain the hardware deals
-// workgroup j of the first residency to CU j % C (C CUs per domain, four workgroups per CU; the
-// later workgroups take the first slots that free up). A CU's time is about the sum of its units'
-// key blocks, so:
+// workgroup j of the first residency to CU j % C (C CUs per domain, S workgroups per CU: 4 for the
+// unbiased head-dim-64 single-split kernel, 1 for the others; the later workgroups take the first
+// slots that free up). A CU's time is about the sum of its units' key blocks, so:
 //   1. sequences sorted by key blocks, longest first (stable), go to the domain with the least work
 //      so far among those not yet full (B/8 each) - the sums per domain come out nearly equal;
 //   2. in each domain, from longest first, pairs of positions are swapped while that lowers the
@@ -110,41 +110,44 @@ int num_cus();
 // against 13 for dealing longest first round-robin; on the hardware, where later workgroups take
 // whichever slot frees first, some CUs still get 13. Measured against the round-robin deal: 34.3 ->
 // 33.8 us for the launch, 120.1 -> 118.6 us for a self + cross pair; step 1 alone measured 34.5 us.
-// The search is bounded (kSearchOps simulated workgroup placements; a miss measured 0.5-1.2 ms of
-// host time at batch 64; the sweep's cross-attention converges in two passes, 0.24M): a launch too large for one pass
-// over the pairs takes the round-robin deal of the longest-first order, and a B that 8 does not
-// divide plain longest first. The result depends on the key lengths only and is cached for the
-// last kScheduleSlots length sets (the DiT runs every block and step with the same prompts, and a
-// classifier-free-guidance caller alternates two sets).
+//
+// Host cost. The search of step 2 is resumable and advances by at most kSearchOpsPerCall simulated
+// workgroup placements per call, so a new set of key lengths costs one bounded step (8 us median on
+// the build host at batch 64, against 0.5-1.2 ms for the whole search): its first launch runs the
+// domain-balanced order of step 1 improved by that step, and each later call with the same lengths
+// continues the search from where the last one stopped until it converges (the batch-64 sweep's
+// cross-attention after 81 calls; the DiT repeats its prompts in all 14 blocks of every step). The
+// whole search is capped at kSearchOps placements; a launch for which one pass over the pairs does
+// not fit takes the round-robin deal of the longest-first order, and a B that 8 does not divide
+// plain longest first. States are kept for the last kScheduleSlots length sets (a guidance caller
+// alternates two), each behind its own mutex: callers with different key lengths never wait for one
+// another, and callers with the same lengths wait at most one step.
 constexpr int64_t kSearchOps = 1 << 19;
-constexpr int kScheduleSlots = 4;
+constexpr int64_t kSearchOpsPerCall = 1 << 11;
+constexpr int kScheduleSlots = 16;
 
-struct ScheduleSlot {
-  int B = 0, Lk = 0, C = 0;
-  int64_t T = 0;
-  int32_t len[sa::kMaxOrder];
-  uint8_t order[sa::kMaxOrder];
+struct ScheduleModel {
+  int B, Lk, C, S;
+  int64_t T;
 };
-struct ScheduleCache {
-  std::mutex mu;
-  int next = 0;  // slot the next miss replaces
-  ScheduleSlot slot[kScheduleSlots];
-};
-ScheduleCache g_schedule;
 
-int64_t simulate_domain(const uint8_t* seq, int n, const int* nb, int T, int C, int64_t* sumsq) {
+int64_t simulate_domain(const uint8_t* seq, int n, const int* nb, int T, int C, int S, int64_t* sumsq) {
   int load[64];
   for (int c = 0; c < C; ++c) load[c] = 0;
-  int j = 0;
+  int j = 0, jc = 0;  // jc = j % C (no division in the loop)
   for (int r = 0; r < n; ++r) {
     const int w = nb[seq[r]];
     for (int t = 0; t < T; ++t, ++j) {
-      if (j < 4 * C) {
-        load[j % C] += w;
+      if (j < S * C) {
+        load[jc] += w;
+        if (++jc == C) jc = 0;
       } else {  // a later workgroup: the slot that frees first, taken as the least loaded CU
-        int best = 0;
-        for (int c = 1; c < C; ++c)
-          if (load[c] < load[best]) best = c;
+        int best = 0, bv = load[0];
+        for (int c = 1; c < C; ++c) {  // branch-free (selects): the comparisons are unpredictable
+          const bool lt = load[c] < bv;
+          bv = lt ? load[c] : bv;
+          best = lt ? c : best;
+        }
         load[best] += w;
       }
     }
@@ -158,81 +161,191 @@ int64_t simulate_domain(const uint8_t* seq, int n, const int* nb, int T, int C, 
   return mx;
 }
 
-void balanced_schedule(const int32_t* len, int B, int Lk, int64_t T, int C, uint8_t* order) {
-  int idx[sa::kMaxOrder], nb[sa::kMaxOrder];
+// The search of step 2 as a resumable state: domain x, pass, pair (u, v), the domain's current
+// heaviest CU and sum of squares, and what it has spent.
+struct ScheduleState {
+  ScheduleModel m;
+  int32_t len[sa::kMaxOrder];
+  uint8_t order[sa::kMaxOrder];
+  int nb[sa::kMaxOrder];
+  int per = 0;
+  int64_t sim_ops = 0;
+  bool done = true;
+  int x = 0, pass = 0, u = 0, v = 0;
+  bool dom_started = false, improved = false;
+  int64_t mx = 0, sq = 0, spent = 0;
+};
+
+// Steps 1 (and the fallbacks) for st.m / st.len: fills st.order and arms the search.
+void schedule_start(ScheduleState& st) {
+  const ScheduleModel& m = st.m;
+  const int B = m.B;
+  int idx[sa::kMaxOrder];
+  int top = 0;
   for (int i = 0; i < B; ++i) {
-    nb[i] = (std::min(std::max(len[i], 0), Lk) + 31) / 32;
-    int j = i;
-    for (; j > 0 && nb[idx[j - 1]] < nb[i]; --j) idx[j] = idx[j - 1];  // insertion sort, stable
-    idx[j] = i;
+    st.nb[i] = (std::min(std::max(st.len[i], 0), m.Lk) + 31) / 32;
+    top = std::max(top, st.nb[i]);
   }
-  if (B % 8 != 0 || nb[idx[0]] == nb[idx[B - 1]]) {  // (all equal: the launch order, i.e. no schedule)
-    for (int j = 0; j < B; ++j) order[j] = (uint8_t)idx[j];
+  // sequences by key blocks, most first, stable: a counting sort (the comparisons of an insertion
+  // sort are unpredictable branches), or a merge sort for very long keys
+  constexpr int kBins = 1024;
+  if (top < kBins) {
+    int start[kBins + 1];
+    for (int v = 0; v <= top + 1; ++v) start[v] = 0;
+    for (int i = 0; i < B; ++i) ++start[top - st.nb[i] + 1];
+    for (int v = 1; v <= top + 1; ++v) start[v] += start[v - 1];
+    for (int i = 0; i < B; ++i) idx[start[top - st.nb[i]]++] = i;
+  } else {
+    for (int i = 0; i < B; ++i) idx[i] = i;
+    std::stable_sort(idx, idx + B, [&](int a, int b) { return st.nb[a] > st.nb[b]; });
+  }
+  st.done = true;
+  if (B % 8 != 0 || st.nb[idx[0]] == st.nb[idx[B - 1]]) {  // (all equal: the launch order, i.e. no schedule)
+    for (int j = 0; j < B; ++j) st.order[j] = (uint8_t)idx[j];
     return;
   }
   const int per = B / 8;
   // Work of one simulation (workgroups, the later ones scanning C CUs) and of one pass over the
   // pairs of every domain; without room for one pass, the round-robin deal.
-  const int64_t units = per * std::min<int64_t>(std::max<int64_t>(T, 1), 1 << 20);
-  const int64_t sim_ops = units + std::max<int64_t>(units - 4 * C, 0) * C;
+  const int64_t units = per * std::min<int64_t>(std::max<int64_t>(m.T, 1), 1 << 20);
+  const int64_t sim_ops = units + std::max<int64_t>(units - (int64_t)m.S * m.C, 0) * m.C;
   const int64_t pairs = (int64_t)per * (per - 1) / 2;
-  if (pairs == 0 || C < 1 || C > 64 || T < 1 || T > (1 << 20) || 8 * pairs * sim_ops > kSearchOps) {
-    for (int j = 0; j < B; ++j) order[(j % 8) * per + j / 8] = (uint8_t)idx[j];
+  if (pairs == 0 || m.C < 1 || m.C > 64 || m.T < 1 || m.T > (1 << 20) || 8 * pairs * sim_ops > kSearchOps) {
+    for (int j = 0; j < B; ++j) st.order[(j % 8) * per + j / 8] = (uint8_t)idx[j];
     return;
   }
   int64_t total[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   int count[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   for (int j = 0; j < B; ++j) {
-    int best = -1;
-    for (int x = 0; x < 8; ++x)
-      if (count[x] < per && (best < 0 || total[x] < total[best])) best = x;
-    order[best * per + count[best]++] = (uint8_t)idx[j];
-    total[best] += nb[idx[j]];
+    int best = 0;
+    int64_t bv = INT64_MAX;
+    for (int x = 0; x < 8; ++x) {  // branch-free: the least work among the domains not yet full
+      const bool take = count[x] < per && total[x] < bv;
+      bv = take ? total[x] : bv;
+      best = take ? x : best;
+    }
+    st.order[best * per + count[best]++] = (uint8_t)idx[j];
+    total[best] += st.nb[idx[j]];
   }
+  st.per = per;
+  st.sim_ops = sim_ops;
+  st.done = false;
+  st.x = 0;
+  st.dom_started = false;
+}
+
+// Advances the search by at most `budget` simulated placements (one simulation always fits).
+void schedule_advance(ScheduleState& st, int64_t budget) {
   const int64_t domain_ops = kSearchOps / 8;
-  for (int x = 0; x < 8; ++x) {
-    uint8_t* seq = order + x * per;  // longest first within the domain already
-    int64_t sq, spent = sim_ops;
-    int64_t mx = simulate_domain(seq, per, nb, (int)T, C, &sq);
-    bool improved = true;
-    for (int pass = 0; pass < 8 && improved; ++pass) {
-      improved = false;
-      for (int u = 0; u < per; ++u)
-        for (int v = u + 1; v < per && spent + sim_ops <= domain_ops; ++v) {
-          if (nb[seq[u]] == nb[seq[v]]) continue;
-          std::swap(seq[u], seq[v]);
-          int64_t sq2;
-          const int64_t mx2 = simulate_domain(seq, per, nb, (int)T, C, &sq2);
-          spent += sim_ops;
-          if (mx2 < mx || (mx2 == mx && sq2 < sq)) {
-            mx = mx2;
-            sq = sq2;
-            improved = true;
-          } else {
-            std::swap(seq[u], seq[v]);
-          }
-        }
+  const int per = st.per, T = (int)st.m.T, C = st.m.C, S = st.m.S;
+  while (!st.done && budget > 0) {
+    uint8_t* seq = st.order + st.x * per;  // longest first within the domain already
+    if (!st.dom_started) {
+      st.mx = simulate_domain(seq, per, st.nb, T, C, S, &st.sq);
+      st.spent = st.sim_ops;
+      budget -= st.sim_ops;
+      st.dom_started = true;
+      st.pass = 0;
+      st.u = 0;
+      st.v = 1;
+      st.improved = false;
+      continue;
+    }
+    bool next_domain = st.pass >= 8 || st.spent + st.sim_ops > domain_ops;
+    if (!next_domain && st.v >= per) {
+      ++st.u;
+      st.v = st.u + 1;
+    }
+    if (!next_domain && st.u >= per - 1) {  // the end of a pass
+      if (!st.improved) {
+        next_domain = true;
+      } else {
+        ++st.pass;
+        st.u = 0;
+        st.v = 1;
+        st.improved = false;
+        continue;
+      }
+    }
+    if (next_domain) {
+      st.dom_started = false;
+      if (++st.x == 8) st.done = true;
+      continue;
+    }
+    const int u = st.u, v = st.v++;
+    if (st.nb[seq[u]] == st.nb[seq[v]]) continue;
+    std::swap(seq[u], seq[v]);
+    int64_t sq2;
+    const int64_t mx2 = simulate_domain(seq, per, st.nb, T, C, S, &sq2);
+    st.spent += st.sim_ops;
+    budget -= st.sim_ops;
+    if (mx2 < st.mx || (mx2 == st.mx && sq2 < st.sq)) {
+      st.mx = mx2;
+      st.sq = sq2;
+      st.improved = true;
+    } else {
+      std::swap(seq[u], seq[v]);
     }
   }
 }
 
-void cached_schedule(const int32_t* len, int B, int Lk, int64_t T, int C, uint8_t* order) {
-  std::lock_guard<std::mutex> lock(g_schedule.mu);
-  for (const ScheduleSlot& s : g_schedule.slot)
-    if (s.B == B && s.Lk == Lk && s.T == T && s.C == C &&
-        memcmp(s.len, len, (size_t)B * sizeof(int32_t)) == 0) {
-      memcpy(order, s.order, (size_t)B);
-      return;
+uint64_t schedule_key(const int32_t* len, const ScheduleModel& m) {
+  uint64_t h = 1469598103934665603ull;  // FNV-1a over 32-bit words of the model and the lengths
+  auto mix = [&](uint64_t v) {
+    h = (h ^ (uint32_t)v) * 1099511628211ull;
+    h = (h ^ (uint32_t)(v >> 32)) * 1099511628211ull;
+  };
+  mix((uint64_t)m.B);
+  mix((uint64_t)m.Lk);
+  mix((uint64_t)m.C);
+  mix((uint64_t)m.S);
+  mix((uint64_t)m.T);
+  for (int i = 0; i < m.B; ++i) h = (h ^ (uint32_t)len[i]) * 1099511628211ull;
+  return h;
+}
+
+struct ScheduleSlot {
+  std::mutex mu;  // guards st
+  ScheduleState st;
+};
+struct ScheduleCache {
+  std::mutex mu;  // guards key / next only (held for a lookup, never during a search step)
+  uint64_t key[kScheduleSlots] = {};
+  int next = 0;  // slot the next new length set takes
+  ScheduleSlot slot[kScheduleSlots];
+};
+ScheduleCache g_schedule;
+
+bool same_model(const ScheduleModel& a, const ScheduleModel& b) {
+  return a.B == b.B && a.Lk == b.Lk && a.C == b.C && a.S == b.S && a.T == b.T;
+}
+
+// The order for these lengths: the state of their slot advanced by one bounded step (a new slot is
+// started first). Two length sets that share a slot's key, or that race for one slot, restart it:
+// the order copied out always belongs to `len`.
+void cached_schedule(const int32_t* len, const ScheduleModel& m, uint8_t* order) {
+  const uint64_t key = schedule_key(len, m);
+  int i = -1;
+  {
+    std::lock_guard<std::mutex> lock(g_schedule.mu);
+    for (int s = 0; s < kScheduleSlots; ++s)
+      if (g_schedule.key[s] == key) i = s;
+    if (i < 0) {
+      i = g_schedule.next;
+      g_schedule.next = (g_schedule.next + 1) % kScheduleSlots;
+      g_schedule.key[i] = key;
     }
-  balanced_schedule(len, B, Lk, T, C, order);
-  ScheduleSlot& s = g_schedule.slot[g_schedule.next];
-  g_schedule.next = (g_schedule.next + 1) % kScheduleSlots;
-  s.B = B;
-  s.Lk = Lk;
-  s.T = T;
-  s.C = C;
-  memcpy(s.len, len, (size_t)B * sizeof(int32_t));
-  memcpy(s.order, order, (size_t)B);
+  }
+  ScheduleSlot& slot = g_schedule.slot[i];
+  std::lock_guard<std::mutex> lock(slot.mu);
+  ScheduleState& st = slot.st;
+  if (!same_model(st.m, m) || memcmp(st.len, len, (size_t)m.B * sizeof(int32_t)) != 0) {
+    st.m = m;
+    memcpy(st.len, len, (size_t)m.B * sizeof(int32_t));
+    schedule_start(st);
+  }
+  schedule_advance(st, kSearchOpsPerCall);
+  memcpy(order, st.order, (size_t)m.B);
 }
 
 // Resolves an sa_attn_args into kernel parameters; returns SA_OK or an error (message set).
@@ -358,20 +471,9 @@ int resolve(const sa_attn_args* a, sa::AttnParams* p) {
   p->key_len = a->key_len;
   p->key_mask = a->key_mask;
   p->smask = a->B > 1 ? (a->smask > 0 ? a->smask : a->Lk) : 0;
-  // The schedule pays one dependent kernel-argument load per workgroup: used only when the batch
-  // is large enough to queue workgroups (small batches run in one round) and the order is not the
-  // launch order already.
+  // the sequence schedule, if any, is made for the chosen kernel (apply_schedule)
+  p->key_len_host = a->mask_mode == SA_MASK_KEY_LEN ? key_len_host : nullptr;
   p->order_n = 0;
-  if (a->mask_mode == SA_MASK_KEY_LEN && key_len_host && a->B >= 8 && a->B <= sa::kMaxOrder) {
-    // units per sequence of the 128-query flash grid the schedule is made for
-    cached_schedule(key_len_host, a->B, a->Lk, (int64_t)a->H * ((a->Lq + 127) / 128), num_cus() / 8,
-                    p->order);
-    for (int r = 0; r < a->B; ++r)
-      if (p->order[r] != r) {
-        p->order_n = a->B;
-        break;
-      }
-  }
   return SA_OK;
 }
 
@@ -520,11 +622,29 @@ int choose(const sa::AttnParams& p, Choice* c) {
   return SA_OK;
 }
 
+// The sequence schedule of a key-length call whose host copy of the lengths came along: made for the
+// chosen flash kernel (its units per sequence and workgroups per CU), and used only when the batch is
+// large enough to queue workgroups (small batches run in one round) and the order is not the launch
+// order already (the schedule pays one dependent kernel-argument load per workgroup).
+void apply_schedule(sa::AttnParams& p, const Choice& c) {
+  p.order_n = 0;
+  if (c.path != Path::kFlash || p.key_len_host == nullptr || p.B < 8 || p.B > sa::kMaxOrder) return;
+  ScheduleModel m;
+  m.B = p.B;
+  m.Lk = p.Lk;
+  m.C = num_cus() / 8;
+  m.S = sa::flash_mfma_per_cu(p, c.nsplit);
+  const int qt = sa::flash_mfma_unit_queries(c.nsplit);
+  m.T = (int64_t)p.H * ((p.Lq + qt - 1) / qt);
+  cached_schedule(p.key_len_host, m, p.order);
+  for (int r = 0; r < p.B; ++r)
+    if (p.order[r] != r) {
+      p.order_n = p.B;
+      break;
+    }
+}
+
 }  // namespace
-
-extern "C" {
-
-}  // extern "C"
 
 namespace {
 
@@ -560,6 +680,7 @@ int run_attention(const sa_attn_args* args, void* stream, bool own_scratch) {
   Choice c;
   rc = choose(p, &c);
   if (rc != SA_OK) return rc;
+  apply_schedule(p, c);
   hipError_t e;
   if (c.path == Path::kFlash) {
     e = sa::launch_flash_mfma(p, c.nsplit, num_cus(), (hipStream_t)stream);
@@ -737,6 +858,7 @@ int sa_attention_plan(const sa_attn_args* args, sa_attn_plan* plan) {
   Choice c;
   rc = choose(p, &c);
   if (rc != SA_OK) return rc;
+  apply_schedule(p, c);  // as the launch would: the plan reports the order it would use
   // filled in full here, then copied out up to the caller's struct_size
   sa_attn_plan full{};
   sa_attn_plan* const out = plan;

@@ -709,6 +709,19 @@ int64_t flash_mfma_tail_groups(const AttnParams& p, int nsplit, int num_cus, int
   return (int64_t)p.B * p.H * q_sub - *first;
 }
 
+int flash_mfma_unit_queries(int nsplit) { return 32 * (4 / compiled_split(64, nsplit)); }
+
+int flash_mfma_per_cu(const AttnParams& p, int nsplit) {
+  const FlashVariant v = flash_mfma_variant(p, nsplit);
+  const bool four = v.D == 64 && v.nsplit == 1 && v.bias == BIAS_NONE && v.mask != MASK_KEY_MASK;
+  static_assert(kMinBlocksPerCU<64, 1, BIAS_NONE, MASK_KEY_LEN_ORDERED> == 4 &&
+                    kMinBlocksPerCU<64, 2, BIAS_NONE, MASK_KEY_LEN_ORDERED> == 1 &&
+                    kMinBlocksPerCU<128, 1, BIAS_NONE, MASK_KEY_LEN_ORDERED> == 1 &&
+                    kMinBlocksPerCU<64, 1, BIAS_DENSE, MASK_KEY_LEN_ORDERED> == 1,
+                "flash_mfma_per_cu must follow kMinBlocksPerCU");
+  return four ? 4 : 1;
+}
+
 int64_t flash_mfma_workgroups(const AttnParams& p, int nsplit, int num_cus) {
   const int qt = 32 * (4 / compiled_split(p.D, nsplit));
   return (int64_t)p.B * p.H * ((p.Lq + qt - 1) / qt) - flash_mfma_tail_units(p, nsplit, num_cus);

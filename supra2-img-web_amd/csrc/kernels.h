@@ -28,6 +28,9 @@ struct AttnParams {
   const int32_t* key_len;
   const uint8_t* key_mask;
   int64_t smask;
+  // Host copy of key_len (or null): the input of the sequence schedule, which the host makes once
+  // the kernel is chosen. Never read by a kernel.
+  const int32_t* key_len_host;
   // Sequence schedule of the flash kernel: sequence rank r (its position in the launch order)
   // runs sequence order[r] when order_n > 0, sequence r otherwise. Kernel-argument data, so the
   // lookup is a scalar load and needs no device allocation.
@@ -69,8 +72,9 @@ static_assert(sizeof(FlashArgs) == 112, "flash kernel arguments must stay within
 FlashArgs flash_args(const AttnParams& p, int64_t tiles);
 
 // Flash kernel on fp32 MFMA for D in {64, 128} with 16-byte aligned rows.
-// nsplit in {1, 2, 4}: key blocks are split across the 4 waves of a workgroup. num_cus (the
-// device's CU count) sets the start-up stagger of the single-split kernels.
+// nsplit in {1, 2}: key blocks are split across the 4 waves of a workgroup (small head-dim-64
+// launches take flash_small instead). num_cus (the device's CU count) sets the start-up stagger of
+// the single-split kernels.
 hipError_t launch_flash_mfma(const AttnParams& p, int nsplit, int num_cus, hipStream_t stream);
 const char* flash_mfma_name(int D, int nsplit);
 // The flash kernels take 32-bit strides, at most 32767 heads and buckets; other calls take the
@@ -86,6 +90,10 @@ struct FlashVariant {
 FlashVariant flash_mfma_variant(const AttnParams& p, int nsplit);
 // Workgroups of that launch.
 int64_t flash_mfma_workgroups(const AttnParams& p, int nsplit, int num_cus);
+// Queries per workgroup of the flash kernel with this key split, and the workgroups of that variant
+// one CU holds at once (4 for the unbiased head-dim-64 single-split kernels, 1 for the others).
+int flash_mfma_unit_queries(int nsplit);
+int flash_mfma_per_cu(const AttnParams& p, int nsplit);
 // Units (128-query tiles) of a flash launch that go to a second launch (0 = none), the kernel of
 // that launch, and the work items [*first, *first + count) it runs (returns count): 32-query groups
 // of flash_small, or 64-query units of the 2-way key-split flash kernel.

@@ -2,16 +2,21 @@
 
 The library orders the sequences of a key-length call before launching the flash kernel: longest
 first by key blocks, balanced over the 8 L2 domains (domain x takes the ranks [x*B/8, (x+1)*B/8)),
-then a bounded search per domain against a model of how the hardware deals workgroups to CUs.
-These tests read the order back through the revision-2 plan fields and check what must hold of it
-whatever the search finds: a permutation, equal work per domain, the model's heaviest CU no worse
-than the plain round-robin deal (and at the bound for the benchmark's sweep), the documented
-fallbacks exactly, and no schedule where none is used. The GPU tests check that the order never
-changes a result (tests/test_schedule_gpu.py)."""
+then a search per domain against a model of how the hardware deals workgroups to CUs, which
+advances by a bounded step per call with the same lengths (a plan query counts as a call: it
+reports the order that launch would use). These tests read the order back through the revision-2
+plan fields and check what must hold of it whatever the search finds: a permutation, equal work per
+domain, the model's heaviest CU no worse than the plain round-robin deal (and at the bound for the
+benchmark's sweep once settled), the documented fallbacks exactly, no schedule where none is used,
+the host time of a new length set, and callers on several threads. The GPU tests check that the
+order never changes a result (tests/test_schedule_gpu.py)."""
 
 from __future__ import annotations
 
 import ctypes
+import gc
+import threading
+import time
 
 import numpy as np
 import pytest
@@ -21,14 +26,30 @@ from supra_attn import _lib, workloads
 CUS = 256  # the plan query's CU count without a GPU (the MI355X value)
 
 
-def plan_for(key_len, H=9, Lq=256, Lk=128, host=True) -> _lib.AttnPlan:
+# Calls after which a search has used its whole budget (2^19 placements, 2^11 per call) and stopped.
+SETTLE_CALLS = 260
+
+
+def args_for(key_len, H=9, Lq=256, Lk=128, host=True, D=64) -> _lib.AttnArgs:
     B = len(key_len)
     kl = np.ascontiguousarray(key_len, dtype=np.int32)
-    hd = H * 64
-    a = _lib.AttnArgs(B=B, H=H, D=64, Lq=Lq, Lk=Lk, q=1 << 20, k=1 << 34, v=1 << 38, o=1 << 42, ldq=hd, ldk=hd, ldv=hd,
+    hd = H * D
+    a = _lib.AttnArgs(B=B, H=H, D=D, Lq=Lq, Lk=Lk, q=1 << 20, k=1 << 34, v=1 << 38, o=1 << 42, ldq=hd, ldk=hd, ldv=hd,
                       ldo=hd, sq=Lq * hd, sk=Lk * hd, sv=Lk * hd, so=Lq * hd, scale=0.125,
                       mask_mode=_lib.SA_MASK_KEY_LEN, key_len=1 << 46, key_len_host=kl.ctypes.data if host else None)
     a._keep = kl
+    return a
+
+
+def plan_for(key_len, H=9, Lq=256, Lk=128, host=True, D=64) -> _lib.AttnPlan:
+    return _lib.plan(args_for(key_len, H, Lq, Lk, host, D))
+
+
+def settled_plan(key_len, **kw) -> _lib.AttnPlan:
+    """The plan once the search for these lengths has run to its end."""
+    a = args_for(key_len, **kw)
+    for _ in range(SETTLE_CALLS - 1):
+        _lib.plan(a)
     return _lib.plan(a)
 
 
@@ -41,8 +62,8 @@ def longest_first(key_len, Lk=128):
     return sorted(range(len(nb)), key=lambda i: -nb[i])  # Python's sort is stable
 
 
-def heaviest_cu(order, nb, units, C=CUS // 8):
-    """The dispatch model, per L2 domain: local workgroup j of the first residency (4 per CU) on CU
+def heaviest_cu(order, nb, units, C=CUS // 8, S=4):
+    """The dispatch model, per L2 domain: local workgroup j of the first residency (S per CU) on CU
     j % C, each later one on the CU with the fewest key blocks so far; returns the heaviest CU's."""
     B = len(order)
     per = B // 8
@@ -52,7 +73,7 @@ def heaviest_cu(order, nb, units, C=CUS // 8):
         j = 0
         for r in range(x * per, (x + 1) * per):
             for _ in range(units):
-                c = j % C if j < 4 * C else int(np.argmin(load))
+                c = j % C if j < S * C else int(np.argmin(load))
                 load[c] += nb[order[r]]
                 j += 1
         worst = max(worst, int(load.max()))
@@ -61,7 +82,7 @@ def heaviest_cu(order, nb, units, C=CUS // 8):
 
 def test_sweep_schedule_is_balanced():
     kl = workloads.sweep_key_lengths()
-    p = plan_for(kl)
+    p = settled_plan(kl)
     assert p.mask_variant == _lib.SA_MASK_VARIANT_KEY_LEN_SCHEDULED
     assert p.order_n == 64
     order = list(p.sequence_order[:64])
@@ -86,7 +107,11 @@ def test_sweep_schedule_is_balanced():
 def test_searched_schedules(B):
     rng = np.random.default_rng(B)
     kl = rng.integers(0, 129, size=B)
-    p = plan_for(kl)
+    first = plan_for(kl)  # one bounded step: balanced over the domains already
+    p = settled_plan(kl)
+    for q in (first, p):
+        o = list(q.sequence_order[:q.order_n])
+        assert q.order_n == B and sorted(o) == list(range(B))
     order = list(p.sequence_order[:p.order_n])
     assert p.order_n == B and sorted(order) == list(range(B))
     nb = blocks(kl)
@@ -141,11 +166,116 @@ def test_no_schedule_where_none_is_used():
 
 
 def test_cached_schedules_repeat():
+    """A settled search gives the same order on every later call; sets interleaved with others
+    (fewer than the 16 states kept) keep their own progress; a set whose state was reused by 16 newer
+    sets starts again and settles on the same order."""
     rng = np.random.default_rng(9)
     sets = [rng.integers(0, 129, size=64) for _ in range(6)]
-    first = [list(plan_for(kl).sequence_order[:64]) for kl in sets]  # more sets than the cache holds
+    settled = [list(settled_plan(kl).sequence_order[:64]) for kl in sets]
     again = [list(plan_for(kl).sequence_order[:64]) for kl in reversed(sets)]
-    assert first == list(reversed(again))
+    assert settled == list(reversed(again))
+    # interleaved: each set advances only on its own calls and settles where it does alone
+    fresh = [rng.integers(0, 129, size=64) for _ in range(4)]
+    alone = [list(settled_plan(kl).sequence_order[:64]) for kl in fresh]
+    for _ in range(16):
+        plan_for(rng.integers(0, 129, size=64))
+    args = [args_for(kl) for kl in fresh]
+    for _ in range(SETTLE_CALLS):
+        for a in args:
+            _lib.plan(a)
+    assert [list(_lib.plan(a).sequence_order[:64]) for a in args] == alone
+
+
+def test_new_length_sets_cost_a_bounded_step():
+    """100 consecutive calls with new key lengths at batch 64 (each a miss) cost at most 20 us of host
+    time, against 0.5-1.2 ms for a whole search. Timed on the thread's CPU clock around the C call
+    with prebuilt arguments. A shared host interrupts a few calls of any kind (a plan query without a
+    host copy, which makes no schedule, shows the same rare 10-40 us outliers), so the bound is
+    asserted on 95 of the 100 calls, the median at 10 us, and a round is run again (up to 3) when the
+    bound misses."""
+    lib = _lib.load()
+    rng = np.random.default_rng(21)
+    out = _lib.AttnPlan()
+    fn = lib.sa_attention_plan
+    fn(ctypes.byref(args_for(rng.integers(1, 129, size=64))), ctypes.byref(out))  # warm
+    rounds = []
+    gc_was = gc.isenabled()
+    gc.disable()
+    try:
+        for _ in range(3):
+            args = [args_for(rng.integers(1, 129, size=64)) for _ in range(100)]
+            ts = []
+            for a in args:
+                t0 = time.thread_time_ns()
+                rc = fn(ctypes.byref(a), ctypes.byref(out))
+                ts.append(time.thread_time_ns() - t0)
+                assert rc == _lib.SA_OK and out.order_n == 64
+            ts = np.sort(np.array(ts)) / 1e3
+            rounds.append((float(np.median(ts)), float(ts[94])))
+            if rounds[-1][1] <= 20.0:
+                break
+    finally:
+        if gc_was:
+            gc.enable()
+    med, p95 = min(rounds, key=lambda r: r[1])
+    assert p95 <= 20.0 and med <= 10.0, rounds
+
+
+def test_callers_on_several_threads():
+    """Eight threads, each with its own lengths, call concurrently (ctypes drops the GIL for the
+    call): every order is a permutation, and each settles where it does on one thread."""
+    rng = np.random.default_rng(33)
+    sets = [rng.integers(0, 129, size=64) for _ in range(8)]
+    want = [list(settled_plan(kl).sequence_order[:64]) for kl in sets]
+    for _ in range(16):  # start every set again from step 1
+        plan_for(rng.integers(0, 129, size=64))
+    got = [None] * 8
+    errors = []
+
+    def run(i):
+        try:
+            a = args_for(sets[i])
+            for _ in range(SETTLE_CALLS):
+                p = _lib.plan(a)
+                assert sorted(p.sequence_order[:64]) == list(range(64))
+            got[i] = list(_lib.plan(a).sequence_order[:64])
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append(e)
+
+    threads = [threading.Thread(target=run, args=(i,)) for i in range(8)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    assert got == want
+
+
+def test_schedule_follows_the_chosen_kernel():
+    """The schedule models the kernel that runs: the 2-way key-split flash kernel (64-query units,
+    one workgroup per CU) for a batch too small for 2 waves per SIMD, head dim 128 likewise; the
+    small-launch kernel (at most 256 query groups) gets none."""
+    rng = np.random.default_rng(17)
+    kl = rng.integers(0, 129, size=8 * 3)
+    p = settled_plan(kl)  # 24 x 9 x 8 = 1728 groups of 32 queries: the split kernel
+    assert p.key_split == 2 and p.order_n == 24
+    nb = blocks(kl)
+    lf = longest_first(kl)
+    rr = [None] * 24
+    for j, i in enumerate(lf):
+        rr[(j % 8) * 3 + j // 8] = i
+    assert heaviest_cu(list(p.sequence_order[:24]), nb, 9 * 4, S=1) <= heaviest_cu(rr, nb, 9 * 4, S=1)
+    kl = rng.integers(0, 129, size=64)
+    p = settled_plan(kl, D=128)  # 64 x 9 x 8 groups at head dim 128: single split, one workgroup per CU
+    assert p.head_dim == 128 and p.key_split == 1 and p.order_n == 64
+    nb = blocks(kl)
+    lf = longest_first(kl)
+    rr = [None] * 64
+    for j, i in enumerate(lf):
+        rr[(j % 8) * 8 + j // 8] = i
+    assert heaviest_cu(list(p.sequence_order[:64]), nb, 9 * 2, S=1) <= heaviest_cu(rr, nb, 9 * 2, S=1)
+    q = plan_for(rng.integers(0, 129, size=8), H=1)  # 8 x 8 groups: flash_small, no schedule
+    assert q.kernel == _lib.SA_KERNEL_FLASH_SMALL and q.order_n == 0
 
 
 def test_plan_revision_1_is_accepted_and_not_overrun():
