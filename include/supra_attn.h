@@ -52,7 +52,8 @@ extern "C" {
 /* Relative-position bias gathered in-kernel (HF T5 compute_bias, mirrored by
  * app/models/t5.js:55-65): element (b, h, i, j) = bias[bucket_lut[j - i + Lq - 1] * H + h], with
  * bias the [num_buckets, H] table of app/models/t5.js:44 and bucket_lut an int32 device array of
- * Lq + Lk - 1 buckets (fill it with sa_t5_bucket_lut). */
+ * Lq + Lk - 1 buckets (fill it with sa_t5_bucket_lut). A bucket id outside [0, num_buckets) is
+ * clamped into it (every kernel, and sa_t5_position_bias, apply the same rule). */
 #define SA_BIAS_RELPOS 2
 
 /* ---- key masking (on top of the Lk bound) ---- */
@@ -117,7 +118,7 @@ typedef struct sa_attn_args {
 int sa_attention_f32(const sa_attn_args* args, void* stream);
 
 /* Scratch the allocation-free entry point has per GPU: 32 MiB of device memory, held from the
- * library's first such call on that GPU until the process ends. */
+ * library's first use on that GPU (below) until the process ends. */
 #define SA_NOALLOC_SCRATCH_BYTES (32 << 20)
 
 /* sa_attention_f32 for callers that cannot allocate device memory: code under HIP graph capture,
@@ -125,10 +126,14 @@ int sa_attention_f32(const sa_attn_args* args, void* stream);
  * args->workspace and workspace_bytes are ignored: the kernels that merge partial results across
  * workgroups use the library's own per-GPU scratch (a static device array of
  * SA_NOALLOC_SCRATCH_BYTES), and a call that needs more (sa_attention_workspace_bytes) fails with
- * SA_ERR_UNSUPPORTED before any launch. Nothing in the call allocates (the first call on a GPU
- * looks up that GPU's scratch address, once). Every call on one GPU shares its scratch: calls
- * ordered on one stream are fine, calls that overlap on one GPU (other streams, other threads)
- * race. The scratch holds nothing that must start at zero. */
+ * SA_ERR_UNSUPPORTED before any launch. Nothing in the call allocates. The library looks up a
+ * GPU's scratch address (hipGetSymbolAddress, which loads the library's device code on that GPU if
+ * nothing has yet) once, at its first use on that GPU: sa_set_device, sa_malloc, sa_stream_create or
+ * any operator call there. A caller that captures these calls into a HIP graph makes one of those
+ * calls on the GPU before it begins the capture; otherwise the first call in the capture does the
+ * lookup. Every call on one GPU shares its scratch: calls ordered on one stream are fine, calls
+ * that overlap on one GPU (other streams, other threads) race. The scratch holds nothing that must
+ * start at zero. */
 int sa_attention_f32_noalloc(const sa_attn_args* args, void* stream);
 
 /* Device scratch bytes sa_attention_f32 needs for these arguments on the current device (0 for

@@ -656,7 +656,8 @@ constexpr int64_t kScratchBytes = SA_NOALLOC_SCRATCH_BYTES;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 std::atomic<void*> g_scratch[kMaxDevices];
 
-// Device address of the current device's scratch, looked up on the first call on that device.
+// Device address of the current device's scratch, looked up once per device: at the library's
+// first use on that device (prepare_device), or failing that by the first allocation-free call.
 int scratch_address(void** out) {
   const int dev = current_device();
   if (dev < 0) return fail(SA_ERR_HIP, "no current HIP device");
@@ -671,9 +672,26 @@ int scratch_address(void** out) {
   return SA_OK;
 }
 
+// Set-up of the current device at the library's first use there (sa_set_device, sa_malloc,
+// sa_stream_create, any operator call): the scratch address lookup, which may load the library's
+// device code on the device, so that an allocation-free call captured into a HIP graph later does
+// neither. Errors are left to the allocation-free call, which looks up again and reports them.
+void prepare_device() {
+  const int dev = current_device();
+  if (dev < 0 || g_scratch[dev].load(std::memory_order_acquire) != nullptr) return;
+  char err[sizeof(g_err)];
+  const int status = g_status;
+  memcpy(err, g_err, sizeof err);
+  void* ptr = nullptr;
+  (void)scratch_address(&ptr);
+  memcpy(g_err, err, sizeof err);  // the caller's own status stays as it was
+  g_status = status;
+}
+
 // Validates, selects and launches one attention call. The wide-head kernel's merge records go to
 // the caller's workspace, or (own_scratch) to the library's per-GPU scratch.
 int run_attention(const sa_attn_args* args, void* stream, bool own_scratch) {
+  prepare_device();
   sa::AttnParams p;
   int rc = resolve(args, &p);
   if (rc != SA_OK) return rc;
@@ -745,6 +763,7 @@ int64_t sa_attention_workspace_bytes(const sa_attn_args* args) {
 // The linear layer with an optional residual source (resid: rows laid out like y, read by the
 // residual epilogues in place of y; the caller has checked that it does not overlap y).
 static int run_linear(const sa_linear_args* args, const float* resid, void* stream) {
+  prepare_device();
   sa::LinearParams p;
   const int rc = resolve_linear(args, &p);
   if (rc != SA_OK) return rc;
@@ -812,9 +831,11 @@ int sa_vae_attention_f32(const sa_vae_attn_args* a, void* stream) {
   l2.y = a->out;
   // every part is validated before the first launch, so a rejected call launches nothing
   if (!sa_linear_kernel_name(&l1) || !sa_attention_kernel_name(&at) || !sa_linear_kernel_name(&l2)) {
+    // the rejecting part's own status (SA_ERR_UNSUPPORTED, SA_ERR_ALIAS, ...) and message
+    const int why_rc = g_status != SA_OK ? g_status : SA_ERR_INVALID;
     char why[sizeof(g_err)];
     memcpy(why, g_err, sizeof why);
-    return fail(SA_ERR_INVALID, "VAE block: %s", why);
+    return fail(why_rc, "VAE block: %s", why);
   }
   const hipStream_t st = (hipStream_t)stream;
   hipError_t e = sa::launch_groupnorm(a->x, a->gamma, a->beta, n, reinterpret_cast<float*>(ws + L.gn), a->HW, a->C,
@@ -1031,14 +1052,18 @@ int sa_device_count(int32_t* count) {
 
 int sa_set_device(int32_t device) {
   hipError_t e = hipSetDevice(device);
-  return e == hipSuccess ? ok() : hip_fail(e, "hipSetDevice");
+  if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+  prepare_device();
+  return ok();
 }
 
 int sa_malloc(void** ptr, size_t bytes) {
   if (!ptr) return fail(SA_ERR_INVALID, "ptr is NULL");
   *ptr = nullptr;
   hipError_t e = hipMalloc(ptr, bytes == 0 ? 16 : bytes);
-  return e == hipSuccess ? ok() : hip_fail(e, "hipMalloc");
+  if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+  prepare_device();
+  return ok();
 }
 
 int sa_free(void* ptr) {
@@ -1095,7 +1120,9 @@ int sa_stream_create(void** stream) {
   hipStream_t s = nullptr;
   hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
   *stream = s;
-  return e == hipSuccess ? ok() : hip_fail(e, "hipStreamCreateWithFlags");
+  if (e != hipSuccess) return hip_fail(e, "hipStreamCreateWithFlags");
+  prepare_device();
+  return ok();
 }
 
 int sa_stream_destroy(void* stream) {

@@ -7,10 +7,10 @@
 // Work decomposition
 //   A workgroup is 4 wave64s. Each wave owns 32 queries of one (sequence b, head h). With
 //   NSPLIT = 1 the 4 waves cover 128 consecutive queries and share every 32-key K/V tile staged
-//   in LDS. With NSPLIT = 2 or 4 the waves split the key blocks instead (4/NSPLIT query groups of
-//   32, each seeing every NSPLIT-th key block) and their partial softmax states are merged in LDS
-//   at the end: small launches (the B=2 DiT call has only 144 groups of 32 queries) then still
-//   spread over many SIMDs.
+//   in LDS. With NSPLIT = 2 the waves split the key blocks instead (two query groups of 32, each
+//   seeing every other key block) and their partial softmax states are merged in LDS at the end:
+//   launches of under ~2 waves per SIMD then still spread over many SIMDs. (Head-dim-64 launches of
+//   at most 256 query groups, such as the batch-2 DiT calls, take flash_small instead.)
 //
 // Per 32-key block a wave computes the transposed score tile S^T = K Q^T with 32x32x2 fp32 MFMAs:
 //   A operand  K[key = lane%32][d], B operand Q^T[d][query = lane%32], the head dim split between

@@ -136,7 +136,9 @@ __global__ __launch_bounds__(64 * NW, 1) void flash_small_kernel(FlashArgs p) {
     const int k0 = j * 32;
     if constexpr (BIAS == BIAS_RELPOS) {
       const int li = k0 - q0 - 31 + lane + (p.Lq - 1);
-      bb.bucket = (lane < 63 && li >= 0 && li <= p.Lq + p.Lk - 2) ? p.lut[li] : -1;
+      // -1 marks a lane past the LUT (no bias there); bucket ids below 0 clamp to 0, and above the
+      // table to its last row (where used), as in every kernel
+      bb.bucket = (lane < 63 && li >= 0 && li <= p.Lq + p.Lk - 2) ? max(p.lut[li], 0) : -1;
     }
     if constexpr (BIAS == BIAS_DENSE) {
       if (bias_vec && k0 + 32 <= p.Lk) {

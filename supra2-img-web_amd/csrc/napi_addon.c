@@ -68,6 +68,13 @@ static int throw_if(napi_env env, int rc) {
   return 1;
 }
 
+/* Throws the status of the library call that just returned NULL: its own status, or
+ * SA_ERR_INVALID should it ever have left none, so the JS call always throws. */
+static void throw_last(napi_env env) {
+  const int rc = sa_last_status();
+  throw_if(env, rc != SA_OK ? rc : SA_ERR_INVALID);
+}
+
 static int ensure_stream(napi_env env) {
   if (g_stream_ready) return 0;
   if (throw_if(env, sa_stream_create(&g_stream))) return 1;
@@ -448,7 +455,7 @@ static napi_value js_linear(napi_env env, napi_callback_info info) {
   if (fill_linear(env, argv[0], &a, &hs)) return NULL;
   /* validate before touching the device, so a bad call reports its own error on any host */
   if (sa_linear_kernel_name(&a) == NULL) {
-    throw_if(env, sa_last_status());
+    throw_last(env);
     return NULL;
   }
   if (check_linear(env, &a, &hs) || ensure_stream(env)) return NULL;
@@ -464,7 +471,7 @@ static napi_value js_linear_kernel_name(napi_env env, napi_callback_info info) {
   if (fill_linear(env, argv[0], &a, &hs)) return NULL;
   const char* name = sa_linear_kernel_name(&a);
   if (!name) {
-    throw_if(env, sa_last_status());
+    throw_last(env);
     return NULL;
   }
   napi_value r;
@@ -563,7 +570,7 @@ static napi_value js_attention(napi_env env, napi_callback_info info) {
   if (fill_args(env, argv[0], &a, &hs)) return NULL;
   /* validate before touching the device, so a bad call reports its own error on any host */
   if (sa_attention_kernel_name(&a) == NULL) {
-    throw_if(env, sa_last_status());
+    throw_last(env);
     return NULL;
   }
   if (check_attn(env, &a, &hs) || ensure_stream(env)) return NULL;
@@ -596,7 +603,7 @@ static napi_value js_kernel_name(napi_env env, napi_callback_info info) {
   if (fill_args(env, argv[0], &a, &hs)) return NULL;
   const char* name = sa_attention_kernel_name(&a);
   if (!name) {
-    throw_if(env, sa_last_status());
+    throw_last(env);
     return NULL;
   }
   napi_value r;

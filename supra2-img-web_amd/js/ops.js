@@ -88,6 +88,20 @@ function nativeArgs(o, out) {
   return args;
 }
 
+// Profiler flops of a call as the reference counts them (app/gpu/ops.js:116: 4*Lq*Lk*D*H, where a
+// caller passes each sample its own key count), summed over the B sequences: a key-length call
+// counts each sequence's attended keys, min(max(keyLen[b], 0), Lk), when their host copy came along
+// (keyLenHost); without it the padded Lk (the device lengths are not read back for a count).
+function attentionFlops(o) {
+  var B = def(o.B, 1);
+  var keys = B * o.Lk;
+  if (o.keyLen && o.keyLenHost) {
+    keys = 0;
+    for (var b = 0; b < B; b++) keys += Math.min(Math.max(o.keyLenHost[b] | 0, 0), o.Lk);
+  }
+  return 4 * o.Lq * keys * o.D * o.H;
+}
+
 function attention(gpu, o) {
   var B = def(o.B, 1);
   var out = o.out || gpu.empty([B * o.Lq, o.H * o.D]);
@@ -102,8 +116,7 @@ function attention(gpu, o) {
     args.workspaceBytes = wsBytes;
   }
   try {
-    // flops as the reference's profiler counts them (app/gpu/ops.js:116), over the B sequences
-    gpu.op({ name: "attention", flops: 4 * B * o.Lq * o.Lk * o.D * o.H }, function () {
+    gpu.op({ name: "attention", flops: attentionFlops(o) }, function () {
       gpu.native.attention(args);
     });
   } finally {

@@ -401,6 +401,36 @@ checkAsync("profiler: per-operator ms and flops (app/gpu/device.js:272-325)", fu
   });
 });
 
+checkAsync("profiler: key-length calls count attended keys (app/gpu/ops.js:116 with each sample's own Lk)", function () {
+  var f = timedNative();
+  return device.GPU.create({ native: f, profile: true }).then(function (gpu) {
+    var q = gpu.empty([4 * 256, 576]);
+    var kv = gpu.empty([4 * 128, 1152]);
+    var kl = gpu.empty([4], "i32");
+    var lens = new Int32Array([77, 1, 200, -3]);  // clamped to [0, Lk]: 77 + 1 + 128 + 0 keys
+    var base = { q: q, k: kv, v: kv, B: 4, Lq: 256, Lk: 128, H: 9, D: 64, ldq: 576, ldk: 1152, ldv: 1152,
+                 kOff: 0, vOff: 576, sq: 256 * 576, sk: 128 * 1152, sv: 128 * 1152, keyLen: kl };
+    sa.attention(gpu, Object.assign({ keyLenHost: lens }, base));
+    return gpu.profiler.report().then(function (rows) {
+      assert.strictEqual(rows[0].flops, 4 * 256 * (77 + 1 + 128 + 0) * 64 * 9);
+      gpu.profiler.reset();
+      sa.attention(gpu, base);  // no host copy: the padded length
+      return gpu.profiler.report();
+    }).then(function (rows) {
+      assert.strictEqual(rows[0].flops, 4 * 256 * 4 * 128 * 64 * 9);
+      gpu.profiler.reset();
+      // the batched DiT helper hands its host lengths over: the count is the per-sample calls' sum
+      var ctx = { kv: kv, keyLen: kl, lens: new Int32Array([77, 1, 5, 128]), B: 4, Lmax: 128 };
+      sa.dit.crossAttention(gpu, q, ctx);
+      return gpu.profiler.report();
+    }).then(function (rows) {
+      var att = rows.filter(function (r) { return r.name === "attention"; })[0];
+      assert.strictEqual(att.flops, 4 * 256 * (77 + 1 + 5 + 128) * 64 * 9);
+      gpu.profiler.destroy();
+    });
+  });
+});
+
 checkAsync("device-lost latch: a HIP error makes every later call throw (app/gpu/device.js:134, 208)", function () {
   var f = fakeNative();
   var gpu = new device.GPU(f);

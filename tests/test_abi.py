@@ -456,6 +456,30 @@ def test_vae_workspace_size():
         ldq=1536, ldk=1536, ldv=1536, scale=0.044))
 
 
+@launches_fake_addresses
+def test_vae_block_passes_on_the_rejecting_part_status():
+    """A VAE block that one of its parts cannot run fails with that part's status, not a generic one:
+    SA_ERR_UNSUPPORTED from the attention (head dim C = 2048 above the generic kernel's 1024) and from
+    the q|k|v projection (K = C = 36, not a multiple of 8, over more rows than its generic kernel's
+    grid); nothing launches either way (fake addresses)."""
+    lib = _lib.load()
+    for over in (dict(HW=64, C=2048, groups=32), dict(HW=1_100_000, C=36, groups=4)):
+        kw = dict(HW=1024, C=512, x=FAKE, gamma=FAKE + (1 << 30), beta=FAKE + (1 << 30) + (1 << 20),
+                  wqkv=FAKE + (2 << 30), wo=FAKE + (3 << 30), out=FAKE + (4 << 30), workspace=FAKE + (5 << 30))
+        kw.update(over)
+        probe = _lib.VaeAttnArgs(**kw)
+        need = lib.sa_vae_attention_workspace_bytes(ctypes.byref(probe))
+        if need < 0:  # the attention part already rejects the sizes
+            assert need == _lib.SA_ERR_UNSUPPORTED
+            kw["workspace_bytes"] = 1 << 30
+        else:
+            kw["workspace_bytes"] = need
+        args = _lib.VaeAttnArgs(**kw)
+        assert lib.sa_vae_attention_f32(ctypes.byref(args), None) == _lib.SA_ERR_UNSUPPORTED, over
+        assert lib.sa_last_status() == _lib.SA_ERR_UNSUPPORTED
+        assert lib.sa_last_error().decode()
+
+
 @pytest.mark.parametrize("over,code", [
     (dict(struct_size=8), _lib.SA_ERR_INVALID),
     (dict(HW=0), _lib.SA_ERR_INVALID),

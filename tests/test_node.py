@@ -30,7 +30,7 @@ def test_shim_and_addon_on_cpu(tmp_path):
     res = subprocess.run([NODE, os.path.join(ROOT, "tests", "node", "shim_cpu.js"), str(f), str(st)],
                          capture_output=True, text=True, timeout=120)
     assert res.returncode == 0, res.stdout + res.stderr
-    assert "all 16 checks passed" in res.stdout
+    assert "all 17 checks passed" in res.stdout
 
 
 def _weights_fixture(tmp_path):

@@ -277,3 +277,43 @@ def test_position_bias_builder(dev):
     _lib.check(_lib.load().sa_t5_position_bias(tb.ptr, lb.ptr, 32, H, Lq, Lk, out.ptr, ctypes.c_void_p(dev.stream)))
     dev.sync()
     np.testing.assert_array_equal(out.read(), orc.dense_relpos_bias(table, lut, H, Lq, Lk))
+
+
+@pytest.mark.parametrize("shape,kernel", [
+    (dict(B=1, H=12, D=64, Lq=128, Lk=128), "flash_small_d64"),          # small launch (48 groups)
+    (dict(B=4, H=12, D=64, Lq=256, Lk=100), "flash_mfma_d64_split2"),    # 384 groups: 2-way key split
+    (dict(B=22, H=12, D=64, Lq=256, Lk=70), "flash_mfma_d64"),           # 2112 groups: single split
+    (dict(B=2, H=4, D=128, Lq=100, Lk=90), "flash_mfma_d128_split2"),
+    (dict(B=2, H=3, D=80, Lq=40, Lk=50), "generic"),
+])
+def test_out_of_range_buckets_clamp_alike_in_every_kernel(dev, shape, kernel):
+    """A bucket LUT holding ids outside [0, num_buckets) (out of contract: sa_t5_bucket_lut never
+    writes one) gives, in every kernel family, bit for bit the result of the LUT clamped into the
+    table, and so does the dense builder."""
+    import ctypes
+
+    c1 = make_call(**shape, scale=1.0, bias_mode=_lib.SA_BIAS_RELPOS, num_buckets=8, seed=5)
+    rng = np.random.default_rng(6)
+    c1.lut = rng.integers(-20, 30, size=c1.lut.shape).astype(np.int32)
+    c2 = make_call(**shape, scale=1.0, bias_mode=_lib.SA_BIAS_RELPOS, num_buckets=8, seed=5)
+    c2.lut = np.clip(c1.lut, 0, 7).astype(np.int32)
+    print(f"[case] clamp {kernel} {shape}", flush=True)
+    s1, s2 = Staged(dev, c1), Staged(dev, c2)
+    try:
+        assert s1.kernel == s2.kernel == kernel
+        o1, o2 = s1.run(), s2.run()
+    finally:
+        s1.release()
+        s2.release()
+    assert np.isfinite(o1).all()
+    np.testing.assert_array_equal(o1, o2)
+    H, Lq, Lk = shape["H"], shape["Lq"], shape["Lk"]
+    tb = dev.from_array(c1.bias)
+    outs = []
+    for lut in (c1.lut, c2.lut):
+        lb = dev.from_array(lut)
+        out = dev.empty((H, Lq, Lk))
+        _lib.check(_lib.load().sa_t5_position_bias(tb.ptr, lb.ptr, 8, H, Lq, Lk, out.ptr, ctypes.c_void_p(dev.stream)))
+        dev.sync()
+        outs.append(out.read())
+    np.testing.assert_array_equal(outs[0], outs[1])

@@ -87,3 +87,82 @@ def test_noalloc_rejects_calls_beyond_its_scratch(dev):
     finally:
         q.release()
         o.release()
+
+
+_GRAPH_CHILD = r"""
+import ctypes, sys
+from ctypes import byref, c_int, c_void_p
+import numpy as np
+from supra_attn import _lib, workloads
+from supra_attn.device import Device
+from supra_attn.runner import Staged
+from cases import make_call
+
+hip = ctypes.CDLL("libamdhip64.so.7")  # the runtime libsupra_attn.so links
+for name, args in (("hipStreamBeginCapture", [c_void_p, c_int]), ("hipStreamEndCapture", [c_void_p, c_void_p]),
+                   ("hipGraphInstantiate", [c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_size_t]),
+                   ("hipGraphLaunch", [c_void_p, c_void_p]), ("hipGraphExecDestroy", [c_void_p]),
+                   ("hipGraphDestroy", [c_void_p])):
+    getattr(hip, name).restype = c_int
+    getattr(hip, name).argtypes = args
+lib = _lib.load()
+dev = Device(0)  # sa_set_device, sa_stream_create: the library's first use on the GPU, before any capture
+s = c_void_p(dev.stream)
+
+def noalloc_args(st):
+    a = _lib.AttnArgs()
+    ctypes.memmove(byref(a), byref(st.args), ctypes.sizeof(a))
+    a.workspace = None
+    a.workspace_bytes = 0
+    return a
+
+big = Staged(dev, workloads.vae_mid(seed=3))           # 8 key chunks merged through the scratch
+small = Staged(dev, make_call(B=1, H=1, D=512, Lq=700, Lk=650, seed=41))
+big.launch(); dev.sync(); ref = big.out.read()         # the workspace call
+small.launch(); dev.sync(); ref_small = small.out.read()
+a_big, a_small = noalloc_args(big), noalloc_args(small)
+print("[graph] capture: the process's first allocation-free call", flush=True)
+graph, exe = c_void_p(), c_void_p()
+assert hip.hipStreamBeginCapture(s, 0) == 0  # global mode: any allocation or sync inside fails
+rc = lib.sa_attention_f32_noalloc(byref(a_big), s)
+assert hip.hipStreamEndCapture(s, byref(graph)) == 0 and graph.value
+assert rc == _lib.SA_OK, lib.sa_last_error()
+assert hip.hipGraphInstantiate(byref(exe), graph, None, None, 0) == 0
+for rep in range(3):
+    big.out.fill_bytes(0xFF)
+    # eager work on the same scratch between replays: a smaller allocation-free call
+    small.out.fill_bytes(0xFF)
+    _lib.check(lib.sa_attention_f32_noalloc(byref(a_small), s))
+    dev.sync()
+    assert np.array_equal(small.out.read().view(np.uint32), ref_small.view(np.uint32)), rep
+    assert hip.hipGraphLaunch(exe, s) == 0
+    dev.sync()
+    got = big.out.read()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"replay {rep}"
+    print(f"[graph] replay {rep} bit-identical", flush=True)
+hip.hipGraphExecDestroy(exe)
+hip.hipGraphDestroy(graph)
+big.release(); small.release()
+print("GRAPH_OK", flush=True)
+"""
+
+
+def test_noalloc_wide_call_in_a_graph_in_a_fresh_process():
+    """In a fresh process, whose first allocation-free call is made under stream capture (after
+    the library's first use on the GPU, which looks up the scratch): the captured wide-head call
+    (VAE shape, 8 key chunks merged through the scratch) replays bit for bit like the workspace
+    call, three times, with an eager allocation-free call on the same scratch between replays."""
+    import os
+    import subprocess
+    import sys
+
+    here = os.path.dirname(os.path.abspath(__file__))
+    root = os.path.dirname(here)
+    env = dict(os.environ)
+    env["PYTHONPATH"] = os.pathsep.join([root, os.path.join(root, "supra2-img-web_amd"), here,
+                                         env.get("PYTHONPATH", "")])
+    print("[case] noalloc graph capture in a child process", flush=True)
+    res = subprocess.run([sys.executable, "-u", "-c", _GRAPH_CHILD], env=env, capture_output=True, text=True,
+                         timeout=110)
+    print(res.stdout[-2000:], res.stderr[-2000:], flush=True)
+    assert res.returncode == 0 and "GRAPH_OK" in res.stdout
