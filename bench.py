@@ -8,7 +8,9 @@ sustained fp32 TFLOP/s (FLOPs = 4*D per attended query/key pair, app/gpu/ops.js:
 
 The same JSON line carries:
   headline     DiT self-attention batch 2 x 9 x 256 x 64: us/call, TFLOP/s, fraction of peak
-  per_config   us/call and TFLOP/s of the other single-call configs (DiT cross, T5, VAE)
+  per_config   us/call and TFLOP/s of the four single-call configs (DiT self and cross at batch 2, T5,
+               VAE), each with the PyTorch fp32 CPU time of the same call on all host threads, the
+               speed-up, and the GPU output's rel-L2 / normwise max relative error against it
   roofline     the dominant kernel (sweep self-attention), timed per launch with HIP events
   cpu_baseline the PyTorch fp32 CPU formulation of tools/reference.py:72-79 on a bounded sample
   callsite / linear / vae_block / weights  the callers and data either side of the operator: batched
@@ -168,6 +170,39 @@ def cpu_baseline(data, seconds: float) -> dict:
                   f"{dt:.2f} s, {dt / steps * 1e3:.1f} ms/step",
         "ms_per_step": dt / steps * 1e3,
     }
+
+
+def config_cpu_leg(name: str, call, gpu_out, min_reps: int = 5, min_seconds: float = 0.5) -> dict:
+    """One single-call config on the CPU, as the reference's oracle runs it: PyTorch fp32 on all host
+    threads, inputs already in host memory, the tools/reference.py:72-79 formulation on the DiT
+    callers' packed layouts (cpu_dit_self / cpu_dit_cross) and the PyTorch fp32 path on the gathered
+    heads for T5 (HF T5 eager: bias + additive key mask) and the VAE call (SDPA). Warm-up call, then
+    the median of at least `min_reps` calls and `min_seconds`. Also the GPU output's rel-L2 and
+    normwise max relative error against that CPU output (tools/check.js:31-44)."""
+    import torch
+
+    from oracle import attention as orc
+
+    B, H, D, Lq = call.B, call.H, call.D, call.Lq
+    if name.startswith("dit_self"):
+        fn = lambda: orc.cpu_dit_self(call).numpy().reshape(B, Lq, H, D)  # noqa: E731
+    elif name.startswith("dit_cross"):
+        fn = lambda: orc.cpu_dit_cross(call).numpy().reshape(B, Lq, H, D)  # noqa: E731
+    else:
+        Q, K, V, bias, valid = orc.gather_call(call)
+        fn = lambda: orc.attention_torch_fp32(Q, K, V, scale=call.scale, bias=bias, valid=valid)  # noqa: E731
+    ref = fn()
+    ts = []
+    t_end = time.perf_counter() + min_seconds
+    while len(ts) < min_reps or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        ref = fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    dt = ts[len(ts) // 2]
+    e = orc.errors(orc.output_view(gpu_out, call), ref)
+    return {"cpu_us_per_call": dt * 1e6, "cpu_tflops": call.flops() / dt / 1e12, "cpu_reps": len(ts),
+            "cpu_threads": torch.get_num_threads(), "rel_l2_vs_cpu": e["rel_l2"], "max_rel_vs_cpu": e["max_rel"]}
 
 
 def callsite_block(dev, s_st, c_st, reps: int = 20) -> dict:
@@ -746,8 +781,15 @@ def main() -> int:
             "flops_per_call": call.flops(),
             "bytes_per_call": call.algorithmic_bytes(),
         }
+        out = st.run()  # one more call, read back for the parity figures
         st.release()
         log(f"{name}: {ms * 1e3:.2f} us/call, {tf:.2f} TFLOP/s via {per_config[name]['kernel']}")
+        if not args.no_cpu:
+            leg = config_cpu_leg(name, call, out)
+            leg["speedup"] = leg["cpu_us_per_call"] / (ms * 1e3)
+            per_config[name].update(leg)
+            log(f"{name}: cpu {leg['cpu_us_per_call']:.1f} us/call ({leg['cpu_threads']} threads), "
+                f"{leg['speedup']:.1f}x; rel_l2 {leg['rel_l2_vs_cpu']:.2e}, max_rel {leg['max_rel_vs_cpu']:.2e}")
     vae = vae_block_timing(dev)
     log(f"vae_block: {vae['us_per_call']:.2f} us/call, {vae['tflops']:.2f} TFLOP/s")
     for s, c in staged:
@@ -809,7 +851,8 @@ def main() -> int:
             "cross_us_per_launch_event_pair_each": round(cross_ms_ev * 1e3, 3),
             "cross_tflops": round(cross_flops / (cross_ms * 1e-3) / 1e12, 3),
         },
-        "per_config": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+        "per_config": {k: {kk: (float(f"{vv:.4g}") if kk.endswith("_vs_cpu") else round(vv, 4) if isinstance(vv, float)
+                            else vv) for kk, vv in v.items()}
                        for k, v in per_config.items()},
         "callsite": callsite,
         "linear": linear,

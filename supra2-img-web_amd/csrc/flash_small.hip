@@ -38,7 +38,6 @@ namespace {
 constexpr float kRescaleSlack = 8.f;  // log2 units: p stays <= 256 between rescales
 constexpr int kD = 64;
 constexpr int kWaves = 4;
-constexpr int kPad = 68;  // floats per query row of a merge record (16-byte chunks spread over banks)
 
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;
@@ -304,13 +303,18 @@ __global__ __launch_bounds__(64 * NW, 1) void flash_small_kernel(FlashArgs p) {
   }
 
   // ---- merge the NW partial states: records in LDS, then every thread combines 4 dims of one query
-  __shared__ __attribute__((aligned(16))) float lds_o[NW * 32 * kPad];
+  // Record rows of kD floats, 16-byte chunk c of row r at c ^ (r & 15): the writes (16 query rows
+  // per 16 lanes, the same chunk each) and the combine reads (whole rows) are both conflict-free.
+  // (Rows padded to 68 floats instead kept the writes conflict-free, but the reads of four padded
+  // rows per wave then stalled 128 cycles per workgroup on bank conflicts, SQ_LDS_BANK_CONFLICT.)
+  __shared__ __attribute__((aligned(16))) float lds_o[NW * 32 * kD];
   __shared__ float lds_m[NW * 32];
   __shared__ float lds_l[NW * 32];
   const float lt = sum_with_partner(l);
   {
     // lane (col, half) holds dims 16g + 8*half + 0..7 of query col in registers 4g..4g+3 of both tiles
-    float* row = lds_o + (wave * 32 + col) * kPad + 8 * half;
+    float* row = lds_o + (wave * 32 + col) * kD;
+    const int sw = col & 15;
 #pragma unroll
     for (int gq = 0; gq < 4; ++gq) {
       f32x4 lo, hi;
@@ -322,8 +326,8 @@ __global__ __launch_bounds__(64 * NW, 1) void flash_small_kernel(FlashArgs p) {
       hi[1] = oacc1[4 * gq + 2];
       hi[2] = oacc0[4 * gq + 3];
       hi[3] = oacc1[4 * gq + 3];
-      *reinterpret_cast<f32x4*>(row + 16 * gq) = lo;
-      *reinterpret_cast<f32x4*>(row + 16 * gq + 4) = hi;
+      *reinterpret_cast<f32x4*>(row + 4 * ((4 * gq + 2 * half) ^ sw)) = lo;
+      *reinterpret_cast<f32x4*>(row + 4 * ((4 * gq + 2 * half + 1) ^ sw)) = hi;
     }
     if (half == 0) {
       lds_m[wave * 32 + col] = m;
@@ -343,7 +347,7 @@ __global__ __launch_bounds__(64 * NW, 1) void flash_small_kernel(FlashArgs p) {
     for (int w = 0; w < NW; ++w) {
       const float a = fast_exp2(lds_m[w * 32 + q] - mt);
       lsum = fmaf(lds_l[w * 32 + q], a, lsum);
-      const f32x4 x = *reinterpret_cast<const f32x4*>(lds_o + (w * 32 + q) * kPad + 4 * c);
+      const f32x4 x = *reinterpret_cast<const f32x4*>(lds_o + (w * 32 + q) * kD + 4 * (c ^ (q & 15)));
       acc[0] = fmaf(x[0], a, acc[0]);
       acc[1] = fmaf(x[1], a, acc[1]);
       acc[2] = fmaf(x[2], a, acc[2]);

@@ -317,3 +317,19 @@ def test_out_of_range_buckets_clamp_alike_in_every_kernel(dev, shape, kernel):
         dev.sync()
         outs.append(out.read())
     np.testing.assert_array_equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("D,Lq,Lk,bias,mask,batched", [
+    (256, 70, 300, _lib.SA_BIAS_DENSE, _lib.SA_MASK_KEY_MASK, True),
+    (512, 129, 250, _lib.SA_BIAS_DENSE, _lib.SA_MASK_KEY_MASK, False),
+    (512, 33, 65, _lib.SA_BIAS_DENSE, _lib.SA_MASK_KEY_LEN, True),
+    (256, 1, 257, _lib.SA_BIAS_DENSE, _lib.SA_MASK_NONE, False),
+    (512, 100, 90, _lib.SA_BIAS_RELPOS, _lib.SA_MASK_KEY_MASK, False),
+])
+def test_wide_heads_with_a_bias(dev, D, Lq, Lk, bias, mask, batched):
+    """A score bias at head dims 256 and 512 (which the reference's unfused chain serves at any head
+    dim, app/gpu/ops.js:119-147) runs on the generic kernel: ragged Lq/Lk, key masks and key lengths,
+    shared and per-sequence dense biases, the relative-position gather."""
+    call = make_call(B=2, H=2, D=D, Lq=Lq, Lk=Lk, bias_mode=bias, mask_mode=mask, dense_bias_batched=batched,
+                     key_mask_p=0.6, seed=D + Lq + Lk)
+    run_checked(dev, call, expect_kernel="generic")
