@@ -158,6 +158,8 @@ const char* sa_attention_kernel_name(const sa_attn_args* args);
 #define SA_KERNEL_GENERIC 3 /* generic_kernel (any head dim <= 1024, any alignment) */
 #define SA_KERNEL_FLASH_SMALL 4 /* flash_small_kernel<key_split waves, bias_mode, mask_variant>: head dim 64,
                                    one workgroup per 32 queries, for launches of at most 256 such groups */
+#define SA_KERNEL_FLASH_SMALL16 5 /* flash_small16_kernel<bias_mode, mask_variant>: head dim 64, one workgroup
+                                     (key_split 4 waves) per 16 queries, for launches of at most 256 such groups */
 /* mask_variant beyond the SA_MASK_* values: per-sequence key lengths plus the host
  * sequence schedule (SA_MASK_KEY_LEN with key_len_host, 8 <= B <= 256, order not the identity) */
 #define SA_MASK_VARIANT_KEY_LEN_SCHEDULED 3

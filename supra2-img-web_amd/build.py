@@ -23,7 +23,7 @@ INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(LIBDIR, "libsupra_attn.so")
 ADDON = os.path.join(LIBDIR, "supra_attn.node")
 
-HIP_SOURCES = ["api.hip", "flash_mfma.hip", "flash_small.hip", "wide_mfma.hip", "generic.hip", "linear_mfma.hip", "groupnorm.hip",
+HIP_SOURCES = ["api.hip", "flash_mfma.hip", "flash_small.hip", "flash_small16.hip", "wide_mfma.hip", "generic.hip", "linear_mfma.hip", "groupnorm.hip",
                "safetensors.hip", "weights.hip"]
 ARCH = "gfx950"
 # Packed FP32 instructions are kept out of the device code (they are emitted from plain float

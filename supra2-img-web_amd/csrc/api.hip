@@ -546,7 +546,7 @@ int64_t align256(int64_t b) { return (b + 255) & ~(int64_t)255; }
 // gives the same kernel choice as the real workspace, which is 16-byte aligned at least).
 int vae_plan(const sa_vae_attn_args* a, char* ws, VaeLayout* L, sa_attn_args* at);
 
-enum class Path { kFlash, kSmall, kWide, kGeneric };
+enum class Path { kFlash, kSmall, kSmall16, kWide, kGeneric };
 
 struct Choice {
   Path path;
@@ -595,9 +595,12 @@ int choose(const sa::AttnParams& p, Choice* c) {
     const int64_t units = (int64_t)p.B * p.H * ((p.Lq + 31) / 32);
     const int nblk = (p.Lk + 31) / 32;
     if (p.D == 64 && units <= 256 && nblk >= 2) {
-      c->path = Path::kSmall;
+      // groups of 16 queries while they still fit one workgroup per CU: twice the CUs, half the
+      // MFMA cycles per key block on each SIMD
+      const bool g16 = sa::flash_small16_workgroups(p) <= 256;
+      c->path = g16 ? Path::kSmall16 : Path::kSmall;
       c->nsplit = sa::flash_small_waves(p);
-      c->name = sa::flash_small_name(c->nsplit);
+      c->name = g16 ? sa::flash_small16_name() : sa::flash_small_name(c->nsplit);
       return SA_OK;
     }
     int nsplit = 1;
@@ -704,6 +707,8 @@ int run_attention(const sa_attn_args* args, void* stream, bool own_scratch) {
     e = sa::launch_flash_mfma(p, c.nsplit, num_cus(), (hipStream_t)stream);
   } else if (c.path == Path::kSmall) {
     e = sa::launch_flash_small(p, (hipStream_t)stream);
+  } else if (c.path == Path::kSmall16) {
+    e = sa::launch_flash_small16(p, (hipStream_t)stream);
   } else if (c.path == Path::kWide) {
     float* ws = nullptr;
     if (c.wide.ws_floats > 0) {
@@ -904,12 +909,13 @@ int sa_attention_plan(const sa_attn_args* args, sa_attn_plan* plan) {
       int64_t first = 0;
       plan->tail_workgroups = sa::flash_mfma_tail_groups(p, c.nsplit, num_cus(), &first);
     }
-  } else if (c.path == Path::kSmall) {
-    plan->kernel = SA_KERNEL_FLASH_SMALL;
+  } else if (c.path == Path::kSmall || c.path == Path::kSmall16) {
+    const bool g16 = c.path == Path::kSmall16;
+    plan->kernel = g16 ? SA_KERNEL_FLASH_SMALL16 : SA_KERNEL_FLASH_SMALL;
     plan->head_dim = p.D;
     plan->key_split = c.nsplit;
     plan->keys_per_step = 32 * c.nsplit;
-    plan->workgroups = sa::flash_small_workgroups(p);
+    plan->workgroups = g16 ? sa::flash_small16_workgroups(p) : sa::flash_small_workgroups(p);
   } else if (c.path == Path::kWide) {
     plan->kernel = SA_KERNEL_WIDE;
     plan->head_dim = p.D;
@@ -931,9 +937,10 @@ int sa_attention_plan(const sa_attn_args* args, sa_attn_plan* plan) {
 }
 
 int32_t sa_attention_variant_count(void) {
-  // flash variants, small-launch variants, the wide kernel (D 256, 512 x no mask / key lengths),
-  // then generic
-  return sa::flash_mfma_variants(nullptr, 0) + sa::flash_small_variants(nullptr, 0) + 4 + 1;
+  // flash variants, small-launch variants (32-query, then 16-query groups), the wide kernel (D 256,
+  // 512 x no mask / key lengths), then generic
+  return sa::flash_mfma_variants(nullptr, 0) + sa::flash_small_variants(nullptr, 0) +
+         sa::flash_small16_variants(nullptr, 0) + 4 + 1;
 }
 
 int sa_attention_variant(int32_t index, sa_attn_plan* plan) {
@@ -944,6 +951,7 @@ int sa_attention_variant(int32_t index, sa_attn_plan* plan) {
                 sizeof(sa_attn_plan));
   const int nflash = sa::flash_mfma_variants(nullptr, 0);
   const int nsmall = sa::flash_small_variants(nullptr, 0);
+  const int nsmall16 = sa::flash_small16_variants(nullptr, 0);
   if (index < 0 || index >= sa_attention_variant_count())
     return fail(SA_ERR_INVALID, "variant index %d outside [0, %d)", index, sa_attention_variant_count());
   // filled in full here, then copied out up to the caller's struct_size
@@ -964,7 +972,20 @@ int sa_attention_variant(int32_t index, sa_attn_plan* plan) {
     memcpy(out, plan, size);
     return ok();
   }
-  if (index >= nflash) index -= nsmall;
+  if (index >= nflash + nsmall && index < nflash + nsmall + nsmall16) {
+    sa::FlashVariant v[64];
+    if (sa::flash_small16_variants(v, 64) > 64) return fail(SA_ERR_UNSUPPORTED, "variant table overflow");
+    const sa::FlashVariant& x = v[index - nflash - nsmall];
+    plan->kernel = SA_KERNEL_FLASH_SMALL16;
+    plan->head_dim = x.D;
+    plan->key_split = x.nsplit;
+    plan->bias_mode = x.bias;
+    plan->mask_variant = x.mask;
+    plan->name = sa::flash_small16_name();
+    memcpy(out, plan, size);
+    return ok();
+  }
+  if (index >= nflash) index -= nsmall + nsmall16;
   if (index < nflash) {
     sa::FlashVariant v[128];
     static_assert(sizeof(v) / sizeof(v[0]) >= 60, "variant table");

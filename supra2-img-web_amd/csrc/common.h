@@ -41,6 +41,18 @@ __device__ __forceinline__ float sum_with_partner(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// The same over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (v_permlane16_swap pairs lanes l and l ^ 16):
+// in the 16x16 MFMA accumulator layout they hold one column in its four row groups. Every one of
+// the four lanes gets the same bits (the additions are commutative).
+__device__ __forceinline__ float max_over_rows4(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return max_with_partner(max_nan(__uint_as_float(r[0]), __uint_as_float(r[1])));
+}
+__device__ __forceinline__ float sum_over_rows4(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return sum_with_partner(__uint_as_float(r[0]) + __uint_as_float(r[1]));
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Waits until at most N of this wave's vector-memory loads (LDS copies included) are outstanding:

@@ -115,6 +115,14 @@ const char* flash_small_name(int nw);
 int flash_small_variants(FlashVariant* out, int cap);
 hipError_t launch_flash_small(const AttnParams& p, hipStream_t stream);
 
+// Small launches with head dim 64 in groups of 16 queries (csrc/flash_small16.hip): one workgroup of
+// 4 waves per 16 queries of one (sequence, head), v_mfma_f32_16x16x4f32; variants <bias, mask> as
+// for flash_small.
+int64_t flash_small16_workgroups(const AttnParams& p);
+const char* flash_small16_name();
+int flash_small16_variants(FlashVariant* out, int cap);
+hipError_t launch_flash_small16(const AttnParams& p, hipStream_t stream);
+
 // Wide heads (D = 256 or 512, no bias, optional key lengths): head dim split across the waves of
 // a workgroup, keys split across workgroups, partials merged by a second kernel via a workspace.
 constexpr int kWideMaxChunks = 16;

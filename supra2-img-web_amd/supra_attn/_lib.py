@@ -103,6 +103,7 @@ SA_KERNEL_FLASH = 1
 SA_KERNEL_WIDE = 2
 SA_KERNEL_GENERIC = 3
 SA_KERNEL_FLASH_SMALL = 4
+SA_KERNEL_FLASH_SMALL16 = 5
 SA_MASK_VARIANT_KEY_LEN_SCHEDULED = 3
 
 

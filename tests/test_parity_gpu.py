@@ -280,7 +280,8 @@ def test_position_bias_builder(dev):
 
 
 @pytest.mark.parametrize("shape,kernel", [
-    (dict(B=1, H=12, D=64, Lq=128, Lk=128), "flash_small_d64"),          # small launch (48 groups)
+    (dict(B=1, H=12, D=64, Lq=128, Lk=128), "flash_small16_d64"),        # small launch (96 groups of 16)
+    (dict(B=3, H=12, D=64, Lq=128, Lk=128), "flash_small_d64"),          # small launch (144 groups of 32)
     (dict(B=4, H=12, D=64, Lq=256, Lk=100), "flash_mfma_d64_split2"),    # 384 groups: 2-way key split
     (dict(B=22, H=12, D=64, Lq=256, Lk=70), "flash_mfma_d64"),           # 2112 groups: single split
     (dict(B=2, H=4, D=128, Lq=100, Lk=90), "flash_mfma_d128_split2"),

@@ -254,7 +254,7 @@ def test_callers_on_several_threads():
 def test_schedule_follows_the_chosen_kernel():
     """The schedule models the kernel that runs: the 2-way key-split flash kernel (64-query units,
     one workgroup per CU) for a batch too small for 2 waves per SIMD, head dim 128 likewise; the
-    small-launch kernel (at most 256 query groups) gets none."""
+    small-launch kernels (at most 256 query groups) get none."""
     rng = np.random.default_rng(17)
     kl = rng.integers(0, 129, size=8 * 3)
     p = settled_plan(kl)  # 24 x 9 x 8 = 1728 groups of 32 queries: the split kernel
@@ -274,8 +274,10 @@ def test_schedule_follows_the_chosen_kernel():
     for j, i in enumerate(lf):
         rr[(j % 8) * 8 + j // 8] = i
     assert heaviest_cu(list(p.sequence_order[:64]), nb, 9 * 2, S=1) <= heaviest_cu(rr, nb, 9 * 2, S=1)
-    q = plan_for(rng.integers(0, 129, size=8), H=1)  # 8 x 8 groups: flash_small, no schedule
+    q = plan_for(rng.integers(0, 129, size=8), H=3)  # 8 x 3 x 8 groups of 32: flash_small, no schedule
     assert q.kernel == _lib.SA_KERNEL_FLASH_SMALL and q.order_n == 0
+    q = plan_for(rng.integers(0, 129, size=8), H=1)  # 8 x 16 groups of 16: flash_small16, no schedule
+    assert q.kernel == _lib.SA_KERNEL_FLASH_SMALL16 and q.order_n == 0
 
 
 def test_plan_revision_1_is_accepted_and_not_overrun():

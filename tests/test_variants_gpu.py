@@ -27,23 +27,25 @@ def test_variant_parity(dev, variant):
     check_call(dev, call, host, variant)
 
 
+@pytest.mark.parametrize("kernel,Lq", [(_lib.SA_KERNEL_FLASH_SMALL, 200), (_lib.SA_KERNEL_FLASH_SMALL16, 100)],
+                         ids=["small", "small16"])
 @pytest.mark.parametrize("bias,batched,mask", [
     (_lib.SA_BIAS_DENSE, False, _lib.SA_MASK_NONE),
     (_lib.SA_BIAS_DENSE, True, _lib.SA_MASK_KEY_MASK),
     (_lib.SA_BIAS_NONE, False, _lib.SA_MASK_KEY_MASK),
 ], ids=["dense", "dense_batched_keymask", "keymask"])
-def test_small_kernel_aligned_operand_rows(dev, bias, batched, mask):
+def test_small_kernel_aligned_operand_rows(dev, kernel, Lq, bias, batched, mask):
     """Lk = 252: every dense-bias and key-mask row starts 16 (4) bytes aligned, so the small-launch
-    kernel reads whole blocks of them with vector loads and the last, partial block (keys 224..251)
+    kernels read whole blocks of them with vector loads and the last, partial block (keys 224..251)
     element by element; Lk = 250 in the variant cases covers the misaligned rows."""
-    call = make_call(B=8, H=4, D=64, Lq=100, Lk=252, seed=77 + bias + 3 * mask, bias_mode=bias, mask_mode=mask,
-                     dense_bias_batched=batched, name=f"small_aligned_b{bias}_m{mask}")
+    call = make_call(B=8, H=4, D=64, Lq=Lq, Lk=252, seed=77 + bias + 3 * mask, bias_mode=bias, mask_mode=mask,
+                     dense_bias_batched=batched, name=f"small_aligned_k{kernel}_b{bias}_m{mask}")
     if call.key_mask is not None:
         call.key_mask[0, :] = 0
         call.key_mask[1, 3] = 1  # a row whose only attended key sits inside a vector-loaded run
         call.key_mask[1, :3] = 0
         call.key_mask[1, 4:] = 0
-    check_call(dev, call, False, (_lib.SA_KERNEL_FLASH_SMALL, 64, 4, bias, 2 if mask else 0))
+    check_call(dev, call, False, (kernel, 64, 4, bias, 2 if mask else 0))
 
 
 def check_call(dev, call, host, variant):

@@ -1,4 +1,4 @@
-"""One attention call per compiled flash-kernel variant <D, key_split, bias, mask>.
+"""One attention call per compiled flash-kernel and small-launch-kernel variant <kernel, D, key_split, bias, mask>.
 
 Each call has the shape real callers give that variant (T5 batches with the relative-position
 bias, DiT-sized batches, head dim 128 with every bias and mask), ragged Lq and Lk (not multiples
@@ -19,14 +19,16 @@ from cases import make_call
 
 # (kernel, D, key_split) -> (B, H, Lq, Lk): every B >= 8 (the scheduled key-length variant needs it),
 # and ceil(Lk / 32) >= 2 * key_split: at least two steps (two blocks) for the last splitting wave.
-FLASH, SMALL = _lib.SA_KERNEL_FLASH, _lib.SA_KERNEL_FLASH_SMALL
+FLASH, SMALL, SMALL16 = _lib.SA_KERNEL_FLASH, _lib.SA_KERNEL_FLASH_SMALL, _lib.SA_KERNEL_FLASH_SMALL16
 SHAPES = {
     (FLASH, 64, 1): (48, 12, 123, 123),   # T5-like batch of prompts (48 x 12 heads, 4 query tiles of 128)
     (FLASH, 64, 2): (16, 12, 200, 150),
     (FLASH, 128, 1): (32, 8, 250, 100),   # head dim 128 (the reference's fused gate admits it, ops.js:112)
     (FLASH, 128, 2): (8, 2, 100, 150),
-    (SMALL, 64, 4): (8, 4, 100, 250),     # 128 groups of 32 queries, 8 key blocks: two per wave
+    (SMALL, 64, 4): (8, 4, 200, 250),     # 224 groups of 32 queries (416 of 16), 8 key blocks: two per wave
+    (SMALL16, 64, 4): (8, 4, 100, 250),   # 224 groups of 16 queries, 8 key blocks: two per wave
 }
+KERNEL_NAMES = {FLASH: "flash", SMALL: "small", SMALL16: "small16"}
 
 MASK_NAMES = {0: "none", 1: "key_len", 2: "key_mask", 3: "key_len_scheduled"}
 BIAS_NAMES = {0: "none", 1: "dense", 2: "relpos"}
@@ -59,7 +61,7 @@ def call_for(kernel: int, D: int, split: int, bias: int, mask: int, seed: int = 
     call = make_call(B=B, H=H, D=D, Lq=Lq, Lk=Lk, seed=seed, scale=scale, packed=(D == 64 and bias == 0),
                      bias_mode=bias, mask_mode=mask_mode, key_len=kl,
                      dense_bias_batched=(bias == _lib.SA_BIAS_DENSE and split == 1),
-                     name=f"{'small' if kernel == SMALL else 'flash'}_d{D}_s{split}_{BIAS_NAMES[bias]}_{MASK_NAMES[mask]}")
+                     name=f"{KERNEL_NAMES[kernel]}_d{D}_s{split}_{BIAS_NAMES[bias]}_{MASK_NAMES[mask]}")
     if mask_mode == _lib.SA_MASK_KEY_MASK:
         call.key_mask[0, :] = 0  # a sequence with no attended key: zeros
     return call, mask == 3
@@ -105,11 +107,11 @@ def fake_args(call, host_key_len: bool) -> _lib.AttnArgs:
 def flash_variants() -> list[tuple]:
     """(kernel, D, key_split, bias, mask) of every compiled flash and small-launch variant."""
     return [(v.kernel, v.head_dim, v.key_split, v.bias_mode, v.mask_variant) for v in _lib.variants()
-            if v.kernel in (FLASH, SMALL)]
+            if v.kernel in (FLASH, SMALL, SMALL16)]
 
 
 def variant_id(v) -> str:
-    return "%s_d%d_s%d_b%d_m%d" % ((("small" if v[0] == SMALL else "flash"),) + tuple(v[1:]))
+    return "%s_d%d_s%d_b%d_m%d" % ((KERNEL_NAMES[v[0]],) + tuple(v[1:]))
 
 
 def steps_per_wave(call, split: int) -> tuple:
