@@ -115,10 +115,11 @@ def test_key_len_including_zero(dev):
 
 PADDING_CASES = [
     # (B, H, D, Lq, Lk, host copy of the lengths): the 4-per-CU flash kernel with and without the
-    # schedule, the small-launch kernel, head dim 128, and the wide kernels
+    # schedule, both small-launch kernels, head dim 128, and the wide kernels
     (64, 9, 64, 256, 128, True),
     (64, 9, 64, 256, 128, False),
-    (6, 2, 64, 64, 128, False),
+    (6, 2, 64, 64, 128, False),     # 48 groups of 16 queries: the 16-query small-launch kernel
+    (8, 9, 64, 64, 128, False),     # 144 groups of 32 (288 of 16): the 32-query small-launch kernel
     (32, 8, 128, 256, 160, True),
     (2, 1, 512, 96, 300, False),
     (2, 2, 256, 64, 200, False),
