@@ -594,10 +594,10 @@ int choose(const sa::AttnParams& p, Choice* c) {
     // blocks across two waves of each workgroup.
     const int64_t units = (int64_t)p.B * p.H * ((p.Lq + 31) / 32);
     const int nblk = (p.Lk + 31) / 32;
-    if (p.D == 64 && units <= 256 && nblk >= 2) {
-      // groups of 16 queries while they still fit one workgroup per CU: twice the CUs, half the
-      // MFMA cycles per key block on each SIMD
-      const bool g16 = sa::flash_small16_workgroups(p) <= 256;
+    if (p.D == 64 && units <= sa::kSmallLaunchCUs && nblk >= 2) {
+      // groups of 16 queries while they still fit one workgroup per CU (short sequences packed to
+      // make them fit): twice the CUs, half the MFMA cycles per key block on each SIMD
+      const bool g16 = sa::flash_small16_workgroups(p) <= sa::kSmallLaunchCUs;
       c->path = g16 ? Path::kSmall16 : Path::kSmall;
       c->nsplit = sa::flash_small_waves(p);
       c->name = g16 ? sa::flash_small16_name() : sa::flash_small_name(c->nsplit);
@@ -916,6 +916,7 @@ int sa_attention_plan(const sa_attn_args* args, sa_attn_plan* plan) {
     plan->key_split = c.nsplit;
     plan->keys_per_step = 32 * c.nsplit;
     plan->workgroups = g16 ? sa::flash_small16_workgroups(p) : sa::flash_small_workgroups(p);
+    if (g16) plan->mask_variant = sa::flash_small16_variant(p).mask;
   } else if (c.path == Path::kWide) {
     plan->kernel = SA_KERNEL_WIDE;
     plan->head_dim = p.D;

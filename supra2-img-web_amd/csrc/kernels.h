@@ -40,8 +40,9 @@ struct AttnParams {
 
 enum { BIAS_NONE = 0, BIAS_DENSE = 1, BIAS_RELPOS = 2 };
 enum { MASK_NONE = 0, MASK_KEY_LEN = 1, MASK_KEY_MASK = 2 };
-// Flash-kernel variant only (never an ABI value): key lengths plus the sequence schedule in
-// AttnParams::order, so that the plain key-length variant does not read the schedule at all.
+// Variant only (never an ABI value): key lengths plus a launch shaped by their host copy. Flash
+// kernel: the sequence schedule in AttnParams::order, so that the plain key-length variant does not
+// read the schedule at all. 16-query small-launch kernel: sequences packed by their key blocks.
 constexpr int MASK_KEY_LEN_ORDERED = 3;
 
 // Arguments of the flash kernels, packed into 112 bytes: the runtime starts launches with at most
@@ -115,10 +116,17 @@ const char* flash_small_name(int nw);
 int flash_small_variants(FlashVariant* out, int cap);
 hipError_t launch_flash_small(const AttnParams& p, hipStream_t stream);
 
+// Launches of at most this many workgroups run one per CU on MI355X (the small-launch kernels).
+constexpr int kSmallLaunchCUs = 256;
+
 // Small launches with head dim 64 in groups of 16 queries (csrc/flash_small16.hip): one workgroup of
-// 4 waves per 16 queries of one (sequence, head), v_mfma_f32_16x16x4f32; variants <bias, mask> as
-// for flash_small.
+// 4 waves per 16 queries of one (sequence, head), v_mfma_f32_16x16x4f32; variants <bias, mask> with
+// mask in {MASK_NONE, MASK_KEY_LEN, MASK_KEY_MASK, MASK_KEY_LEN_ORDERED}. The last packs sequences
+// of at most two key blocks (host key lengths, B <= 16) at 2 or 1 waves per 16-query group, so
+// their workgroups hold 2 or 4 groups, where that makes a launch of more than kSmallLaunchCUs
+// workgroups fit.
 int64_t flash_small16_workgroups(const AttnParams& p);
+FlashVariant flash_small16_variant(const AttnParams& p);
 const char* flash_small16_name();
 int flash_small16_variants(FlashVariant* out, int cap);
 hipError_t launch_flash_small16(const AttnParams& p, hipStream_t stream);

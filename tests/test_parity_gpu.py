@@ -119,6 +119,8 @@ PADDING_CASES = [
     (64, 9, 64, 256, 128, True),
     (64, 9, 64, 256, 128, False),
     (6, 2, 64, 64, 128, False),     # 48 groups of 16 queries: the 16-query small-launch kernel
+    (6, 4, 64, 200, 128, True),     # 312 groups of 16: the short sequences packed, 2 waves per group
+    (2, 9, 64, 256, 128, True),     # the batch-2 DiT cross shape, packed
     (8, 9, 64, 64, 128, False),     # 144 groups of 32 (288 of 16): the 32-query small-launch kernel
     (32, 8, 128, 256, 160, True),
     (2, 1, 512, 96, 300, False),

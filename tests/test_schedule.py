@@ -274,8 +274,13 @@ def test_schedule_follows_the_chosen_kernel():
     for j, i in enumerate(lf):
         rr[(j % 8) * 8 + j // 8] = i
     assert heaviest_cu(list(p.sequence_order[:64]), nb, 9 * 2, S=1) <= heaviest_cu(rr, nb, 9 * 2, S=1)
-    q = plan_for(rng.integers(0, 129, size=8), H=3)  # 8 x 3 x 8 groups of 32: flash_small, no schedule
+    q = plan_for(rng.integers(65, 129, size=8), H=3)  # 8 x 3 x 8 groups of 32: flash_small, no schedule
     assert q.kernel == _lib.SA_KERNEL_FLASH_SMALL and q.order_n == 0
+    # with short sequences among them, packed into fewer 16-query workgroups (3 x (4 x 16 + 2 x 8 +
+    # 2 x 4) = 228): flash_small16, no order
+    q = plan_for([100, 5, 40, 128, 0, 20, 70, 33], H=3)
+    assert q.kernel == _lib.SA_KERNEL_FLASH_SMALL16 and q.order_n == 0
+    assert q.mask_variant == _lib.SA_MASK_VARIANT_KEY_LEN_SCHEDULED
     q = plan_for(rng.integers(0, 129, size=8), H=1)  # 8 x 16 groups of 16: flash_small16, no schedule
     assert q.kernel == _lib.SA_KERNEL_FLASH_SMALL16 and q.order_n == 0
 

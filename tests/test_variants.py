@@ -15,7 +15,7 @@ def test_every_compiled_variant_is_enumerated_once():
     assert len(flash) == len(set(flash))
     assert sum(v[0] == _lib.SA_KERNEL_FLASH for v in flash) == 48  # D 64, 128 x splits 1, 2 x 3 biases x 4 masks
     assert sum(v[0] == SMALL for v in flash) == 9                  # 4 waves x 3 biases x 3 masks
-    assert sum(v[0] == SMALL16 for v in flash) == 9                # likewise, 16-query groups
+    assert sum(v[0] == SMALL16 for v in flash) == 12               # 16-query groups: 3 masks + packed key lengths
     assert sum(v.kernel == _lib.SA_KERNEL_WIDE for v in vs) == 4
     assert sum(v.kernel == _lib.SA_KERNEL_GENERIC for v in vs) == 1
     assert all(v.name for v in vs)

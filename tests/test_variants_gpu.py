@@ -6,19 +6,13 @@ reach every compiled variant."""
 
 from __future__ import annotations
 
-import numpy as np
 import pytest
 
-from oracle import attention as orc
 from supra_attn import _lib
-from supra_attn.runner import Staged
 from cases import make_call
-from variant_cases import call_for, flash_variants, variant_id
+from variant_cases import call_for, check_call, flash_variants, variant_id
 
 pytestmark = pytest.mark.gpu
-
-TOL = 1e-5
-SENTINEL = np.float32(-12345.5)
 
 
 @pytest.mark.parametrize("variant", flash_variants(), ids=variant_id)
@@ -46,33 +40,3 @@ def test_small_kernel_aligned_operand_rows(dev, kernel, Lq, bias, batched, mask)
         call.key_mask[1, :3] = 0
         call.key_mask[1, 4:] = 0
     check_call(dev, call, False, (kernel, 64, 4, bias, 2 if mask else 0))
-
-
-def check_call(dev, call, host, variant):
-    print(f"[case] {call.name} B={call.B} H={call.H} D={call.D} Lq={call.Lq} Lk={call.Lk}", flush=True)
-    st = Staged(dev, call, out_fill=SENTINEL, host_key_len=host)
-    try:
-        assert _lib.plan(st.args).variant() == variant
-        out = st.run()
-    finally:
-        st.release()
-    got = orc.output_view(out, call)
-    e = orc.errors(got, orc.reference_torch(call))
-    assert e["finite"], call.name
-    assert e["rel_l2"] <= TOL and e["max_rel"] <= TOL, f"{call.name} vs torch fp32: {e}"
-    e64 = orc.errors(got, orc.reference_fp64(call))
-    assert e64["rel_l2"] <= TOL and e64["max_rel"] <= TOL, f"{call.name} vs fp64: {e64}"
-    # rows of a sequence with no attended key are zeros
-    if call.key_len is not None:
-        empty = np.asarray(call.key_len) == 0
-        assert (got[empty] == 0).all()
-    if call.key_mask is not None:
-        empty = ~(np.asarray(call.key_mask) != 0).any(axis=1)
-        assert (got[empty] == 0).all()
-    # nothing written outside the output rows
-    ldo = call.args.get("ldo", 0) or call.H * call.D
-    written = np.zeros(out.size, dtype=bool)
-    idx = orc.heads(np.arange(out.size), B=call.B, L=call.Lq, H=call.H, D=call.D, off=call.args.get("o_off", 0),
-                    ld=ldo, sb=call.args.get("so", 0))
-    written[idx.reshape(-1)] = True
-    assert (out.reshape(-1)[~written] == SENTINEL).all()

@@ -17,6 +17,9 @@ import numpy as np
 from supra_attn import _lib
 from cases import make_call
 
+TOL = 1e-5
+SENTINEL = np.float32(-12345.5)
+
 # (kernel, D, key_split) -> (B, H, Lq, Lk): every B >= 8 (the scheduled key-length variant needs it),
 # and ceil(Lk / 32) >= 2 * key_split: at least two steps (two blocks) for the last splitting wave.
 FLASH, SMALL, SMALL16 = _lib.SA_KERNEL_FLASH, _lib.SA_KERNEL_FLASH_SMALL, _lib.SA_KERNEL_FLASH_SMALL16
@@ -28,6 +31,9 @@ SHAPES = {
     (SMALL, 64, 4): (8, 4, 200, 250),     # 224 groups of 32 queries (416 of 16), 8 key blocks: two per wave
     (SMALL16, 64, 4): (8, 4, 100, 250),   # 224 groups of 16 queries, 8 key blocks: two per wave
 }
+# the 16-query kernel's packed key-length variant: 280 groups of 16 queries, more than the 256 CUs,
+# until the empty and the 5-key sequence take 2 waves per group (250 workgroups)
+SMALL16_PACKED = (8, 5, 100, 250)
 KERNEL_NAMES = {FLASH: "flash", SMALL: "small", SMALL16: "small16"}
 
 MASK_NAMES = {0: "none", 1: "key_len", 2: "key_mask", 3: "key_len_scheduled"}
@@ -48,7 +54,7 @@ def key_lengths(rng, B: int, Lk: int, split: int) -> np.ndarray:
 def call_for(kernel: int, D: int, split: int, bias: int, mask: int, seed: int = 0):
     """(call, host_key_len) for the variant; host_key_len says whether the host copy of the key
     lengths goes with the call (it selects the scheduled variant)."""
-    B, H, Lq, Lk = SHAPES[(kernel, D, split)]
+    B, H, Lq, Lk = SMALL16_PACKED if (kernel, mask) == (SMALL16, 3) else SHAPES[(kernel, D, split)]
     seed = seed + 10000 * kernel + 1000 * D + 100 * split + 10 * bias + mask
     rng = np.random.default_rng(seed)
     mask_mode = {0: _lib.SA_MASK_NONE, 1: _lib.SA_MASK_KEY_LEN, 2: _lib.SA_MASK_KEY_MASK,
@@ -123,3 +129,51 @@ def steps_per_wave(call, split: int) -> tuple:
         kv = call.Lk
     nblk = (kv + 31) // 32
     return (nblk + split - 1) // split, (nblk - (split - 1) + split - 1) // split
+
+
+def check_call(dev, call, host, variant, poison_padding=False):
+    """Runs `call` on the GPU (host_key_len = host) after checking that the library picks `variant`;
+    the output against the PyTorch fp32 CPU path and the float64 brute force (both <= 1e-5,
+    relative L2 and normwise max), zero rows for sequences with no attended key, and nothing
+    written outside the output rows. poison_padding: the references are taken first, then every K
+    and V row past a sequence's key length is filled with NaN and Inf (separate K and V arrays)."""
+    from oracle import attention as orc
+    from supra_attn.runner import Staged
+
+    ref = orc.reference_torch(call)
+    ref64 = orc.reference_fp64(call)
+    if poison_padding:
+        ld = call.args["ldk"]
+        k = call.k.reshape(call.B, call.Lk, ld).copy()
+        v = call.v.reshape(call.B, call.Lk, ld).copy()
+        for b, n in enumerate(np.clip(call.key_len, 0, call.Lk)):
+            k[b, n:] = np.nan
+            v[b, n:] = np.where(np.arange(ld) % 2 == 0, np.inf, np.nan).astype(np.float32)
+        call.k, call.v = k.reshape(-1), v.reshape(-1)
+    print(f"[case] {call.name} B={call.B} H={call.H} D={call.D} Lq={call.Lq} Lk={call.Lk}", flush=True)
+    st = Staged(dev, call, out_fill=SENTINEL, host_key_len=host)
+    try:
+        assert _lib.plan(st.args).variant() == variant
+        out = st.run()
+    finally:
+        st.release()
+    got = orc.output_view(out, call)
+    e = orc.errors(got, ref)
+    assert e["finite"], call.name
+    assert e["rel_l2"] <= TOL and e["max_rel"] <= TOL, f"{call.name} vs torch fp32: {e}"
+    e64 = orc.errors(got, ref64)
+    assert e64["rel_l2"] <= TOL and e64["max_rel"] <= TOL, f"{call.name} vs fp64: {e64}"
+    # rows of a sequence with no attended key are zeros
+    if call.key_len is not None:
+        empty = np.asarray(call.key_len) == 0
+        assert (got[empty] == 0).all()
+    if call.key_mask is not None:
+        empty = ~(np.asarray(call.key_mask) != 0).any(axis=1)
+        assert (got[empty] == 0).all()
+    # nothing written outside the output rows
+    ldo = call.args.get("ldo", 0) or call.H * call.D
+    written = np.zeros(out.size, dtype=bool)
+    idx = orc.heads(np.arange(out.size), B=call.B, L=call.Lq, H=call.H, D=call.D, off=call.args.get("o_off", 0),
+                    ld=ldo, sb=call.args.get("so", 0))
+    written[idx.reshape(-1)] = True
+    assert (out.reshape(-1)[~written] == SENTINEL).all()
