@@ -160,8 +160,11 @@ const char* sa_attention_kernel_name(const sa_attn_args* args);
                                    one workgroup per 32 queries, for launches of at most 256 such groups */
 #define SA_KERNEL_FLASH_SMALL16 5 /* flash_small16_kernel<bias_mode, mask_variant>: head dim 64, one workgroup
                                      (key_split 4 waves) per 16 queries, for launches of at most 256 such groups */
-/* mask_variant beyond the SA_MASK_* values: per-sequence key lengths plus the host
- * sequence schedule (SA_MASK_KEY_LEN with key_len_host, 8 <= B <= 256, order not the identity) */
+/* mask_variant beyond the SA_MASK_* values: per-sequence key lengths plus a launch shaped by their
+ * host copy (SA_MASK_KEY_LEN with key_len_host). FLASH: the host sequence schedule (8 <= B <= 256,
+ * order not the identity). FLASH_SMALL16: sequences of at most 64 keys packed at 2 (or, if that is
+ * not enough, 1) waves per 16-query group, shortest first, until a launch of more than 256 groups
+ * fits 256 workgroups (B <= 16); workgroups then counts the packed grid. */
 #define SA_MASK_VARIANT_KEY_LEN_SCHEDULED 3
 
 typedef struct sa_attn_plan {

@@ -289,14 +289,14 @@ __global__ __launch_bounds__(64 * kNW, 1) void flash_small16_kernel(FlashArgs p)
     if (j + nwg < nblk) {
       load_b(bb1, j + nwg);
       load_k(bb1, j + nwg);
-      load_v(bb1, j + nwg, kv_len);
+      load_v(bb1, j + nwg, kv_len - 1);
     }
     compute(j, bb0);
     if (j + nwg >= nblk) break;
     if (j + 2 * nwg < nblk) {
       load_b(bb0, j + 2 * nwg);
       load_k(bb0, j + 2 * nwg);
-      load_v(bb0, j + 2 * nwg, kv_len);
+      load_v(bb0, j + 2 * nwg, kv_len - 1);
     }
     compute(j + nwg, bb1);
   }

@@ -180,3 +180,29 @@ def test_packed_parity(dev, case, bias):
                      mask_mode=_lib.SA_MASK_KEY_LEN, key_len=np.asarray(kl, dtype=np.int32),
                      dense_bias_batched=(B <= 8), name=f"packed_{name}_b{bias}")
     check_call(dev, call, True, (SMALL16, 64, 4, bias, PACKED), poison_padding=True)
+
+
+# (name, B, H, Lq, Lk, device key lengths, host copy): the host copy calls long sequences short, so
+# they are packed anyway and a wave runs several key blocks: 1 wave per group over 4 blocks (two
+# loop iterations with both operand sets), 2 waves per group over 2 blocks each
+STALE_CASES = [
+    ("one_wave_4_blocks", 3, 12, 200, 128, [128, 100, 77], [1, 20, 128]),
+    ("two_waves_2_blocks", 3, 9, 256, 128, [128, 128, 5], [1, 1, 128]),
+]
+
+
+@pytest.mark.parametrize("case", STALE_CASES, ids=[c[0] for c in STALE_CASES])
+def test_stale_cases_are_packed(case):
+    name, B, H, Lq, Lk, kl, host = case
+    p = _lib.plan(args_for(host, H, Lq, Lk))
+    assert (p.kernel, p.mask_variant) == (SMALL16, PACKED) and min(packing(host, H, Lq, Lk)) < 2
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", STALE_CASES, ids=[c[0] for c in STALE_CASES])
+def test_stale_host_copy_costs_speed_not_results(dev, case):
+    """The kernel takes its key lengths from the device, so a wrong host copy only shapes the launch."""
+    name, B, H, Lq, Lk, kl, host = case
+    call = make_call(B=B, H=H, D=64, Lq=Lq, Lk=Lk, seed=400 + B, mask_mode=_lib.SA_MASK_KEY_LEN,
+                     key_len=np.asarray(kl, dtype=np.int32), name=f"stale_{name}")
+    check_call(dev, call, True, (SMALL16, 64, 4, _lib.SA_BIAS_NONE, PACKED), poison_padding=True, host_copy=host)

@@ -131,12 +131,13 @@ def steps_per_wave(call, split: int) -> tuple:
     return (nblk + split - 1) // split, (nblk - (split - 1) + split - 1) // split
 
 
-def check_call(dev, call, host, variant, poison_padding=False):
+def check_call(dev, call, host, variant, poison_padding=False, host_copy=None):
     """Runs `call` on the GPU (host_key_len = host) after checking that the library picks `variant`;
     the output against the PyTorch fp32 CPU path and the float64 brute force (both <= 1e-5,
     relative L2 and normwise max), zero rows for sequences with no attended key, and nothing
     written outside the output rows. poison_padding: the references are taken first, then every K
-    and V row past a sequence's key length is filled with NaN and Inf (separate K and V arrays)."""
+    and V row past a sequence's key length is filled with NaN and Inf (separate K and V arrays).
+    host_copy: a host copy of the key lengths that differs from the device's (a stale one)."""
     from oracle import attention as orc
     from supra_attn.runner import Staged
 
@@ -153,6 +154,9 @@ def check_call(dev, call, host, variant, poison_padding=False):
     print(f"[case] {call.name} B={call.B} H={call.H} D={call.D} Lq={call.Lq} Lk={call.Lk}", flush=True)
     st = Staged(dev, call, out_fill=SENTINEL, host_key_len=host)
     try:
+        if host_copy is not None:
+            st.key_len_host = np.ascontiguousarray(host_copy, dtype=np.int32)
+            st.args.key_len_host = st.key_len_host.ctypes.data
         assert _lib.plan(st.args).variant() == variant
         out = st.run()
     finally:
