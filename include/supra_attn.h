@@ -105,8 +105,11 @@ typedef struct sa_attn_args {
   void* workspace;                    /* device scratch, 16-byte aligned, when the call needs it */
   int64_t workspace_bytes;            /* its size (>= sa_attention_workspace_bytes(args)) */
   /* Revision 3. KEY_LEN: an optional HOST copy of key_len[0..B), read during the call and used
-   * only to schedule the sequences (balanced by key blocks over the device's L2 domains and CUs) when
-   * 8 <= B <= 256; the results come from the device key_len either way, so a stale copy costs
+   * only to shape the launch: the flash kernel schedules the sequences (balanced by key blocks over
+   * the device's L2 domains and CUs) when 8 <= B <= 256, bit for bit neutral; the 16-query
+   * small-launch kernel packs sequences of at most 64 keys into fewer workgroups when B <= 16 and
+   * the launch would exceed one workgroup per CU (the order of the fp32 sums changes, within the
+   * usual rounding). The results come from the device key_len either way, so a stale copy costs
    * speed, never correctness. The DiT caller knows its prompt lengths on the host
    * (app/models/dit.js:137-144). */
   const int32_t* key_len_host;
