@@ -157,7 +157,8 @@ const char* sa_attention_kernel_name(const sa_attn_args* args);
  * (ops.js:111-112) inside the operator; these host-only queries make the equivalent choice of
  * this library inspectable, so tests can show that every compiled variant runs. */
 #define SA_KERNEL_FLASH 1   /* flash_mfma_kernel<head_dim, key_split, bias_mode, mask_variant> */
-#define SA_KERNEL_WIDE 2    /* wide_mfma_kernel<head_dim, mask_variant>, + a merge kernel when key_chunks > 1 */
+#define SA_KERNEL_WIDE 2    /* wide_mfma_kernel<head_dim, bias_mode, mask_variant> (no bias or a dense one), + a
+                                merge kernel when key_chunks > 1 */
 #define SA_KERNEL_GENERIC 3 /* generic_kernel (any head dim <= 1024, any alignment) */
 #define SA_KERNEL_FLASH_SMALL 4 /* flash_small_kernel<key_split waves, bias_mode, mask_variant>: head dim 64,
                                    one workgroup per 32 queries, for launches of at most 256 such groups */

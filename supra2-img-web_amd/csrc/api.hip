@@ -938,10 +938,10 @@ int sa_attention_plan(const sa_attn_args* args, sa_attn_plan* plan) {
 }
 
 int32_t sa_attention_variant_count(void) {
-  // flash variants, small-launch variants (32-query, then 16-query groups), the wide kernel (D 256,
-  // 512 x no mask / key lengths), then generic
+  // flash variants, small-launch variants (32-query, then 16-query groups), the wide kernels (D 256,
+  // 512 x no bias / dense bias x no mask / key lengths / key mask), then generic
   return sa::flash_mfma_variants(nullptr, 0) + sa::flash_small_variants(nullptr, 0) +
-         sa::flash_small16_variants(nullptr, 0) + 4 + 1;
+         sa::flash_small16_variants(nullptr, 0) + sa::wide_mfma_variants(nullptr, 0) + 1;
 }
 
 int sa_attention_variant(int32_t index, sa_attn_plan* plan) {
@@ -998,12 +998,15 @@ int sa_attention_variant(int32_t index, sa_attn_plan* plan) {
     plan->bias_mode = v[index].bias;
     plan->mask_variant = v[index].mask;
     plan->name = sa::flash_mfma_name(v[index].D, v[index].nsplit);
-  } else if (index < nflash + 4) {
-    const int w = index - nflash;
+  } else if (index < nflash + sa::wide_mfma_variants(nullptr, 0)) {
+    sa::FlashVariant v[64];
+    if (sa::wide_mfma_variants(v, 64) > 64) return fail(SA_ERR_UNSUPPORTED, "variant table overflow");
+    const sa::FlashVariant& x = v[index - nflash];
     plan->kernel = SA_KERNEL_WIDE;
-    plan->head_dim = w < 2 ? 256 : 512;
-    plan->mask_variant = (w & 1) ? SA_MASK_KEY_LEN : SA_MASK_NONE;
-    plan->name = sa::wide_mfma_name(plan->head_dim);
+    plan->head_dim = x.D;
+    plan->bias_mode = x.bias;
+    plan->mask_variant = x.mask;
+    plan->name = sa::wide_mfma_name(x.D);
   } else {
     plan->kernel = SA_KERNEL_GENERIC;
     plan->name = "generic";

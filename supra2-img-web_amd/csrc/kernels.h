@@ -131,8 +131,9 @@ const char* flash_small16_name();
 int flash_small16_variants(FlashVariant* out, int cap);
 hipError_t launch_flash_small16(const AttnParams& p, hipStream_t stream);
 
-// Wide heads (D = 256 or 512, no bias, optional key lengths): head dim split across the waves of
-// a workgroup, keys split across workgroups, partials merged by a second kernel via a workspace.
+// Wide heads (D = 256 or 512; no bias or a dense one; no mask, key lengths or a key mask): head dim
+// split across the waves of a workgroup (D = 256) or score blocks dealt to them (D = 512), keys
+// split across workgroups, partials merged by a second kernel via a workspace.
 constexpr int kWideMaxChunks = 16;
 struct WidePlan {
   int q_groups;       // 32-query groups per (sequence, head)
@@ -141,6 +142,8 @@ struct WidePlan {
   int64_t ws_floats;  // workspace floats (0 when nks == 1)
 };
 bool wide_mfma_supported(const AttnParams& p);
+// Every compiled variant <D, 1, bias, mask>, in a fixed order (as flash_mfma_variants).
+int wide_mfma_variants(FlashVariant* out, int cap);
 WidePlan wide_mfma_plan(const AttnParams& p, int num_cus);
 const char* wide_mfma_name(int D);
 hipError_t launch_wide_mfma(const AttnParams& p, const WidePlan& plan, float* ws, hipStream_t stream);

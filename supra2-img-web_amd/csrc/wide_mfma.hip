@@ -49,7 +49,78 @@ __device__ __forceinline__ f32x16 zero16() {
   return z;
 }
 
-template <int D, int NW, int MASK>
+// Dense bias and key mask of one 32-key block in the 32x32 score layout, where lane (col, half)
+// holds query col's keys k0 + 8(r/4) + 4 half + r%4 in score register r: four runs of 4 keys per
+// lane. Loaded before the block's score products (load), folded into the base-2 scores after them
+// (apply). Runs are 16-byte (bias) or 4-byte (mask) loads where the rows allow it and the run lies
+// inside the keys, element loads clamped to the last key otherwise; keys at or past Lk read the
+// last key's entry and are masked by the caller's key bound.
+template <int BIAS, int MASK>
+struct BlockTerms {
+  static constexpr bool kBias = BIAS == BIAS_DENSE;
+  static constexpr bool kMask = MASK == MASK_KEY_MASK;
+  f32x4 bv[kBias ? 4 : 1];
+  uint32_t km[kMask ? 4 : 1];
+
+  struct Rows {
+    const float* brow;     // dense bias row of the lane's query (rows past Lq re-read the last row)
+    const uint8_t* kmask;  // key-mask row of the sequence
+    bool bias_vec, mask_vec;
+    int Lk;
+  };
+  __device__ static Rows rows(const AttnParams& p, int b, int h, int qi) {
+    Rows r;
+    r.Lk = p.Lk;
+    r.brow = nullptr;
+    r.kmask = nullptr;
+    r.bias_vec = r.mask_vec = false;
+    if constexpr (kBias) {
+      r.brow = p.bias + (int64_t)b * p.sbias + ((int64_t)h * p.Lq + min(qi, p.Lq - 1)) * p.Lk;
+      // 16-byte runs: the table 16-byte aligned and every row start a multiple of 4 floats (keys of a
+      // run start at multiples of 4)
+      r.bias_vec = (reinterpret_cast<uintptr_t>(p.bias) & 15) == 0 && (p.Lk & 3) == 0 && (p.sbias & 3) == 0;
+    }
+    if constexpr (kMask) {
+      r.kmask = p.key_mask + (int64_t)b * p.smask;
+      r.mask_vec = (reinterpret_cast<uintptr_t>(r.kmask) & 3) == 0;
+    }
+    return r;
+  }
+  __device__ void load(const Rows& r, int k0, int half) {
+#pragma unroll
+    for (int k4 = 0; k4 < 4; ++k4) {
+      const int kk = k0 + 8 * k4 + 4 * half;  // keys kk .. kk + 3
+      if constexpr (kBias) {
+        if (r.bias_vec && kk + 4 <= r.Lk) {
+          bv[k4] = *reinterpret_cast<const f32x4*>(r.brow + kk);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bv[k4][e] = r.brow[min(kk + e, r.Lk - 1)];
+        }
+      }
+      if constexpr (kMask) {
+        if (r.mask_vec && kk + 4 <= r.Lk) {
+          km[k4] = *reinterpret_cast<const uint32_t*>(r.kmask + kk);
+        } else {
+          uint32_t w = 0;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w |= (uint32_t)r.kmask[min(kk + e, r.Lk - 1)] << (8 * e);
+          km[k4] = w;
+        }
+      }
+    }
+  }
+  // u: base-2 scores; bias in natural units, so it enters times log2(e)
+  __device__ void apply(float* u) const {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      if constexpr (kBias) u[r] = fmaf(bv[r >> 2][r & 3], kLog2e, u[r]);
+      if constexpr (kMask) u[r] = ((km[r >> 2] >> (8 * (r & 3))) & 0xffu) != 0 ? u[r] : -INFINITY;
+    }
+  }
+};
+
+template <int D, int NW, int BIAS, int MASK>
 __global__ __launch_bounds__(64 * NW, 1) void wide_mfma_kernel(AttnParams p, int q_groups, int nks, int chunk, float* ws) {
   constexpr int DS = D / NW;      // head dims per wave
   constexpr int QREG = DS / 2;    // Q values per lane
@@ -89,6 +160,9 @@ __global__ __launch_bounds__(64 * NW, 1) void wide_mfma_kernel(AttnParams p, int
   const int kbeg = kc * chunk;
   const int kend = min(kbeg + chunk, kv_len);
   const int nblk = kend > kbeg ? (kend - kbeg + 31) >> 5 : 0;
+  using Terms = BlockTerms<BIAS, MASK>;
+  constexpr bool kTerms = Terms::kBias || Terms::kMask;
+  const typename Terms::Rows trows = Terms::rows(p, b, h, qi);
 
   float* const kt = lds_k + wave * SLICE;
   float* const vt = lds_v + wave * SLICE;
@@ -151,6 +225,10 @@ __global__ __launch_bounds__(64 * NW, 1) void wide_mfma_kernel(AttnParams p, int
     // own K slice of block j has landed (the last NI loads in flight are V of block j, or the Q
     // loads on the first block); wave-private, so no barrier
     wait_vmcnt<NI>();
+    // the block's bias / mask terms, used after the score exchange (register loads: the compiler
+    // waits for them where they are used)
+    Terms terms;
+    if constexpr (kTerms) terms.load(trows, k0, half);
     // ---- partial scores over this wave's head-dim slice
     f32x16 s = zero16();
     const float* krow = kt + col * DS;
@@ -211,6 +289,7 @@ __global__ __launch_bounds__(64 * NW, 1) void wide_mfma_kernel(AttnParams p, int
       u[4 * k4 + 3] = a[3];
     }
     if (j + 1 < nblk) issue_k(j + 1);  // own K slice consumed: the next one streams in meanwhile
+    if constexpr (kTerms) terms.apply(u);
     if (k0 + 32 > kend) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -314,7 +393,7 @@ __global__ __launch_bounds__(64 * NW, 1) void wide_mfma_kernel(AttnParams p, int
 // partial score tiles through LDS and took the softmax in every wave for every block; one wave
 // per SIMD, its loads software-pipelined. Writes the same partial records as wide_mfma_kernel
 // (merged by wide_merge_kernel), staged through LDS into whole-row stores.
-template <int MASK>
+template <int BIAS, int MASK>
 __global__ __launch_bounds__(256, 1) void wide_rows_kernel(AttnParams p, int q_groups, int nks, int chunk, float* ws) {
   constexpr int D = 512;
   constexpr int NG = D / 8;          // groups of 8 head dims (4 MFMAs) per score tile
@@ -349,6 +428,9 @@ __global__ __launch_bounds__(256, 1) void wide_rows_kernel(AttnParams p, int q_g
   const int kbeg = kc * chunk;
   const int kend = min(kbeg + chunk, kv_len);
   const int rounds = kend > kbeg ? (kend - kbeg + 127) >> 7 : 0;
+  using Terms = BlockTerms<BIAS, MASK>;
+  constexpr bool kTerms = Terms::kBias || Terms::kMask;
+  const typename Terms::Rows trows = Terms::rows(p, b, h, q0 + col);
 
   const float* kbase = p.k + p.k_off + (int64_t)b * p.sk + h * D;
   const float* vbase = p.v + p.v_off + (int64_t)b * p.sv + h * D + wave * DS;
@@ -408,7 +490,9 @@ __global__ __launch_bounds__(256, 1) void wide_rows_kernel(AttnParams p, int q_g
       return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff + 32u * i, 0, 0));
     };
     f32x4 kring[KR];
+    Terms terms;  // the block's bias / mask terms, used after its score products
     if (has_keys) {
+      if constexpr (kTerms) terms.load(trows, kb0, half);
 #pragma unroll
       for (int i = 0; i < KR; ++i) kring[i] = load_k(i);
     }
@@ -458,6 +542,7 @@ __global__ __launch_bounds__(256, 1) void wide_rows_kernel(AttnParams p, int q_g
       });
 #pragma unroll
       for (int r = 0; r < 16; ++r) u[r] = (sa[r] + sb[r]) * p.scale_log2;
+      if constexpr (kTerms) terms.apply(u);
       if (kb0 + 32 > kend) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -653,26 +738,39 @@ __global__ __launch_bounds__(256) void wide_merge_kernel(AttnParams p, int q_gro
 template <int D>
 constexpr int kWideWaves = 4;
 
-template <int D>
-hipError_t launch_d(const AttnParams& p, const WidePlan& plan, float* ws, hipStream_t stream) {
-  constexpr int NW = kWideWaves<D>;
-  const int64_t n = (int64_t)p.B * p.H * plan.q_groups * plan.nks;
-  if (n > 0x7fffffff) return hipErrorInvalidConfiguration;
-  const dim3 grid((unsigned)n), block(64 * NW);
-  if constexpr (D == 512) {
-    if (p.mask_mode == MASK_KEY_LEN)
-      hipLaunchKernelGGL((wide_rows_kernel<MASK_KEY_LEN>), grid, dim3(256), 0, stream, p, plan.q_groups, plan.nks,
-                         plan.chunk, ws);
-    else
-      hipLaunchKernelGGL((wide_rows_kernel<MASK_NONE>), grid, dim3(256), 0, stream, p, plan.q_groups, plan.nks,
-                         plan.chunk, ws);
-  } else if (p.mask_mode == MASK_KEY_LEN)
-    hipLaunchKernelGGL((wide_mfma_kernel<D, NW, MASK_KEY_LEN>), grid, block, 0, stream, p, plan.q_groups, plan.nks,
+template <int D, int BIAS, int MASK>
+void launch_main(const AttnParams& p, const WidePlan& plan, float* ws, dim3 grid, hipStream_t stream) {
+  if constexpr (D == 512)
+    hipLaunchKernelGGL((wide_rows_kernel<BIAS, MASK>), grid, dim3(256), 0, stream, p, plan.q_groups, plan.nks,
                        plan.chunk, ws);
   else
-    hipLaunchKernelGGL((wide_mfma_kernel<D, NW, MASK_NONE>), grid, block, 0, stream, p, plan.q_groups, plan.nks,
-                       plan.chunk, ws);
-  hipError_t e = hipGetLastError();
+    hipLaunchKernelGGL((wide_mfma_kernel<D, kWideWaves<D>, BIAS, MASK>), grid, dim3(64 * kWideWaves<D>), 0, stream, p,
+                       plan.q_groups, plan.nks, plan.chunk, ws);
+}
+
+template <int D, int BIAS>
+hipError_t launch_mask(const AttnParams& p, const WidePlan& plan, float* ws, dim3 grid, hipStream_t stream) {
+  switch (p.mask_mode) {
+    case MASK_NONE: launch_main<D, BIAS, MASK_NONE>(p, plan, ws, grid, stream); break;
+    case MASK_KEY_LEN: launch_main<D, BIAS, MASK_KEY_LEN>(p, plan, ws, grid, stream); break;
+    case MASK_KEY_MASK: launch_main<D, BIAS, MASK_KEY_MASK>(p, plan, ws, grid, stream); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_d(const AttnParams& p, const WidePlan& plan, float* ws, hipStream_t stream) {
+  const int64_t n = (int64_t)p.B * p.H * plan.q_groups * plan.nks;
+  if (n > 0x7fffffff) return hipErrorInvalidConfiguration;
+  const dim3 grid((unsigned)n);
+  hipError_t e;
+  if (p.bias_mode == BIAS_NONE)
+    e = launch_mask<D, BIAS_NONE>(p, plan, ws, grid, stream);
+  else if (p.bias_mode == BIAS_DENSE)
+    e = launch_mask<D, BIAS_DENSE>(p, plan, ws, grid, stream);
+  else
+    return hipErrorInvalidValue;
   if (e != hipSuccess || plan.nks == 1) return e;
   const int64_t threads = (int64_t)p.B * p.H * plan.q_groups * 32 * (D / 4);
   const int64_t blocks = (threads + 255) / 256;
@@ -684,8 +782,19 @@ hipError_t launch_d(const AttnParams& p, const WidePlan& plan, float* ws, hipStr
 }  // namespace
 
 bool wide_mfma_supported(const AttnParams& p) {
-  return (p.D == 256 || p.D == 512) && p.bias_mode == BIAS_NONE &&
-         (p.mask_mode == MASK_NONE || p.mask_mode == MASK_KEY_LEN);
+  return (p.D == 256 || p.D == 512) && (p.bias_mode == BIAS_NONE || p.bias_mode == BIAS_DENSE) &&
+         (p.mask_mode == MASK_NONE || p.mask_mode == MASK_KEY_LEN || p.mask_mode == MASK_KEY_MASK);
+}
+
+int wide_mfma_variants(FlashVariant* out, int cap) {
+  int n = 0;
+  for (int D = 256; D <= 512; D *= 2)
+    for (int bias = BIAS_NONE; bias <= BIAS_DENSE; ++bias)
+      for (int mask = MASK_NONE; mask <= MASK_KEY_MASK; ++mask) {
+        if (n < cap) out[n] = {D, 1, bias, mask};
+        ++n;
+      }
+  return n;
 }
 
 WidePlan wide_mfma_plan(const AttnParams& p, int num_cus) {

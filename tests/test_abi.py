@@ -157,7 +157,12 @@ def test_generic_kernel_for_other_head_dims_and_unaligned_rows():
     vae = _lib.AttnArgs(B=1, H=1, D=512, Lq=1024, Lk=1024, q=FAKE, k=FAKE + (1 << 24), v=FAKE + (2 << 24),
                         o=FAKE + (3 << 24), ldq=512, ldk=512, ldv=512, scale=0.0442)
     assert _lib.kernel_name(vae) == "wide_mfma_d512"
-    assert _lib.kernel_name(good_args(D=512, H=2, ldq=4096, ldk=4096, ldv=4096, ldo=1024, so=256 * 1024, bias_mode=1, bias=FAKE + (2 << 32))) == "generic"
+    wide = dict(D=512, H=2, ldq=4096, ldk=4096, ldv=4096, ldo=1024, so=256 * 1024)
+    # a dense bias and a key mask fuse into the wide kernels; the relative-position gather does not
+    assert _lib.kernel_name(good_args(**wide, bias_mode=1, bias=FAKE + (2 << 32))) == "wide_mfma_d512"
+    assert _lib.kernel_name(good_args(**wide, mask_mode=2, key_mask=FAKE + (2 << 32))) == "wide_mfma_d512"
+    assert _lib.kernel_name(good_args(**wide, bias_mode=2, bias=FAKE + (2 << 32), bucket_lut=FAKE + (3 << 32),
+                                      num_buckets=32)) == "generic"
 
 
 @pytest.mark.parametrize("over,code", [

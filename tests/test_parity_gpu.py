@@ -332,8 +332,9 @@ def test_out_of_range_buckets_clamp_alike_in_every_kernel(dev, shape, kernel):
 ])
 def test_wide_heads_with_a_bias(dev, D, Lq, Lk, bias, mask, batched):
     """A score bias at head dims 256 and 512 (which the reference's unfused chain serves at any head
-    dim, app/gpu/ops.js:119-147) runs on the generic kernel: ragged Lq/Lk, key masks and key lengths,
-    shared and per-sequence dense biases, the relative-position gather."""
+    dim, app/gpu/ops.js:119-147): a dense bias runs on the wide kernels, the relative-position gather
+    on the generic kernel; ragged Lq/Lk, key masks and key lengths, shared and per-sequence dense
+    biases."""
     call = make_call(B=2, H=2, D=D, Lq=Lq, Lk=Lk, bias_mode=bias, mask_mode=mask, dense_bias_batched=batched,
                      key_mask_p=0.6, seed=D + Lq + Lk)
-    run_checked(dev, call, expect_kernel="generic")
+    run_checked(dev, call, expect_kernel=f"wide_mfma_d{D}" if bias == _lib.SA_BIAS_DENSE else "generic")

@@ -6,7 +6,8 @@ from __future__ import annotations
 import pytest
 
 from supra_attn import _lib
-from variant_cases import SMALL, SMALL16, call_for, fake_args, flash_variants, steps_per_wave, variant_id
+from variant_cases import (SMALL, SMALL16, WIDE_SHAPES, call_for, fake_args, flash_variants, steps_per_wave,
+                           variant_id, wide_call_for, wide_variants)
 
 
 def test_every_compiled_variant_is_enumerated_once():
@@ -16,7 +17,7 @@ def test_every_compiled_variant_is_enumerated_once():
     assert sum(v[0] == _lib.SA_KERNEL_FLASH for v in flash) == 48  # D 64, 128 x splits 1, 2 x 3 biases x 4 masks
     assert sum(v[0] == SMALL for v in flash) == 9                  # 4 waves x 3 biases x 3 masks
     assert sum(v[0] == SMALL16 for v in flash) == 12               # 16-query groups: 3 masks + packed key lengths
-    assert sum(v.kernel == _lib.SA_KERNEL_WIDE for v in vs) == 4
+    assert sum(v.kernel == _lib.SA_KERNEL_WIDE for v in vs) == 12  # D 256, 512 x 2 biases x 3 masks
     assert sum(v.kernel == _lib.SA_KERNEL_GENERIC for v in vs) == 1
     assert all(v.name for v in vs)
 
@@ -58,3 +59,22 @@ def test_plan_rejects_like_the_call():
     small.struct_size = 8
     good = _lib.AttnArgs(B=1, H=1, D=64, Lq=1, Lk=1, q=16, k=16, v=16, o=4096, ldq=64, ldk=64, ldv=64, scale=1.0)
     assert _lib.load().sa_attention_plan(ctypes.byref(good), ctypes.byref(small)) == _lib.SA_ERR_INVALID
+
+
+@pytest.mark.parametrize("variant", wide_variants(), ids=lambda v: "wide_d%d_b%d_m%d" % (v[1], v[3], v[4]))
+def test_wide_case_selects_its_variant(variant):
+    call = wide_call_for(*variant)
+    plan = _lib.plan(fake_args(call, False))
+    assert plan.variant() == variant, call.name
+    assert call.Lq % 32 != 0 and call.Lk % 32 != 0, "lengths must be ragged"
+    # the key-chunk split (merge kernel, workspace) and the single-chunk path both run for each head dim
+    assert (plan.key_chunks > 1) == (plan.workspace_bytes > 0)
+
+
+def test_wide_cases_cover_split_and_unsplit():
+    chunks = {}
+    for v in wide_variants():
+        plan = _lib.plan(fake_args(wide_call_for(*v), False))
+        chunks.setdefault(v[1], set()).add(plan.key_chunks > 1)
+    assert chunks == {256: {True, False}, 512: {True, False}}
+    assert len(WIDE_SHAPES) == 6

@@ -10,7 +10,7 @@ import pytest
 
 from supra_attn import _lib
 from cases import make_call
-from variant_cases import call_for, check_call, flash_variants, variant_id
+from variant_cases import call_for, check_call, flash_variants, variant_id, wide_call_for, wide_variants
 
 pytestmark = pytest.mark.gpu
 
@@ -42,3 +42,11 @@ def test_small_kernel_aligned_operand_rows(dev, kernel, Lq, bias, batched, mask)
         call.key_mask[1, :3] = 0
         call.key_mask[1, 4:] = 0
     check_call(dev, call, False, (kernel, 64, 4, bias, 2 if mask else 0))
+
+
+@pytest.mark.parametrize("variant", wide_variants(), ids=lambda v: "wide_d%d_b%d_m%d" % (v[1], v[3], v[4]))
+def test_wide_variant_parity(dev, variant):
+    """Every wide-kernel variant <D, bias, mask>: split into key chunks or not, ragged lengths; key-length
+    cases carry NaN and Inf in every K and V row past a sequence's length."""
+    call = wide_call_for(*variant)
+    check_call(dev, call, False, variant, poison_padding=call.key_len is not None)

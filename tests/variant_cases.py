@@ -73,6 +73,45 @@ def call_for(kernel: int, D: int, split: int, bias: int, mask: int, seed: int = 
     return call, mask == 3
 
 
+# wide kernels: (D, mask) -> (B, H, Lq, Lk), ragged; split into key chunks (merged by a second kernel)
+# or not, both per head dim
+WIDE = _lib.SA_KERNEL_WIDE
+WIDE_SHAPES = {
+    (256, 0): (2, 3, 70, 300),    # 18 query groups: 10 key chunks
+    (256, 1): (32, 4, 100, 90),   # 512 query groups: one chunk each
+    (256, 2): (2, 2, 33, 257),    # 8 query groups: 9 key chunks
+    (512, 0): (1, 1, 129, 250),   # 5 query groups: 2 chunks of one round
+    (512, 1): (16, 1, 500, 300),  # 256 query groups: one chunk of 3 rounds
+    (512, 2): (2, 1, 200, 333),   # 14 query groups: 3 chunks
+}
+
+
+def wide_variants() -> list[tuple]:
+    """(kernel, D, key_split, bias, mask) of every compiled wide-kernel variant."""
+    return [(v.kernel, v.head_dim, v.key_split, v.bias_mode, v.mask_variant) for v in _lib.variants()
+            if v.kernel == WIDE]
+
+
+def wide_call_for(kernel: int, D: int, split: int, bias: int, mask: int, seed: int = 0):
+    """The call for a wide variant: key lengths with 0, 1 and a full sequence where there are
+    enough sequences, a key mask with one sequence fully masked, dense biases shared or per
+    sequence."""
+    B, H, Lq, Lk = WIDE_SHAPES[(D, mask)]
+    seed = seed + 20000 + D + 10 * bias + mask
+    rng = np.random.default_rng(seed)
+    mask_mode = {0: _lib.SA_MASK_NONE, 1: _lib.SA_MASK_KEY_LEN, 2: _lib.SA_MASK_KEY_MASK}[mask]
+    kl = None
+    if mask_mode == _lib.SA_MASK_KEY_LEN:
+        kl = rng.integers(0, Lk + 1, size=B).astype(np.int32)
+        kl[:3] = [0, 1, Lk]
+    call = make_call(B=B, H=H, D=D, Lq=Lq, Lk=Lk, seed=seed, bias_mode=bias, mask_mode=mask_mode, key_len=kl,
+                     key_mask_p=0.6, dense_bias_batched=(bias == _lib.SA_BIAS_DENSE and B > 1 and mask != 1),
+                     name=f"wide_d{D}_{BIAS_NAMES[bias]}_{MASK_NAMES[mask]}")
+    if mask_mode == _lib.SA_MASK_KEY_MASK:
+        call.key_mask[0, :] = 0
+    return call
+
+
 def fake_args(call, host_key_len: bool) -> _lib.AttnArgs:
     """sa_attn_args for `call` with distinct, 16-byte aligned made-up device addresses: enough for
     the host-only plan query (which compares addresses but never dereferences them)."""
