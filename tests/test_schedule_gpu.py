@@ -8,7 +8,9 @@ kernel reads the device key lengths for the arithmetic - and must match the orac
 bar. Cases: the sweep's batch-64 cross-attention (searched), batch 24 (also a multiple of 8), batch
 128 with two query tiles (16 sequences per domain), batch 58 with ragged queries (1044 units over
 unequal L2 domains, plain longest-first order), batch 13 (plain longest-first order) and batch 2
-(below the batch the schedule is used for, so all three runs take the launch order)."""
+(below the batch the schedule is used for; there the host copy may instead pack a short sequence
+into the 16-query small-launch kernel, which runs other arithmetic: that case is held to the
+oracle's bar, not to bits)."""
 
 from __future__ import annotations
 
@@ -38,24 +40,39 @@ def _calls():
 CALLS = list(_calls())
 
 
+def _packed(variant) -> bool:
+    """The 16-query small-launch kernel with sequences packed by their host key lengths."""
+    return variant[0] == _lib.SA_KERNEL_FLASH_SMALL16 and variant[4] == _lib.SA_MASK_VARIANT_KEY_LEN_SCHEDULED
+
+
 @pytest.mark.parametrize("name,call", CALLS, ids=[c[0] for c in CALLS])
 def test_schedule_is_bitwise_neutral(dev, name, call):
+    """Bit for bit wherever the host copy only orders the flash kernel's sequences. A small launch
+    whose host copy packs short sequences (flash_small16.hip) runs other arithmetic than the same call
+    without it (another kernel, or fewer waves per 16-query group): those runs match the oracle at the
+    usual bar instead."""
     print(f"[schedule case] {name} B={call.B} Lq={call.Lq} kernel=", end="", flush=True)
-    outs = {}
+    outs, plans = {}, {}
     for mode in ("host", "none", "stale"):
         st = Staged(dev, call, out_fill=np.nan, host_key_len=mode != "none")
         try:
             if mode == "stale":  # a wrong host copy: reversed lengths, so the order is wrong too
                 st.key_len_host = np.ascontiguousarray(st.key_len_host[::-1])
                 st.args.key_len_host = st.key_len_host.ctypes.data
+            plans[mode] = _lib.plan(st.args).variant()
             if mode == "host":
                 print(st.kernel, flush=True)
             outs[mode] = st.run()
         finally:
             st.release()
-    for mode in ("none", "stale"):
-        np.testing.assert_array_equal(outs[mode].view(np.uint32), outs["host"].view(np.uint32), err_msg=mode)
     ref = orc.reference_torch(call)
+    for mode in ("none", "stale"):
+        same_arithmetic = plans[mode][:4] == plans["host"][:4] and not _packed(plans[mode]) and not _packed(plans["host"])
+        if same_arithmetic:
+            np.testing.assert_array_equal(outs[mode].view(np.uint32), outs["host"].view(np.uint32), err_msg=mode)
+        else:
+            e = orc.errors(orc.output_view(outs[mode], call), ref)
+            assert e["finite"] and e["rel_l2"] <= TOL and e["max_rel"] <= TOL, (mode, plans[mode], e)
     e = orc.errors(orc.output_view(outs["host"], call), ref)
     assert e["finite"] and e["rel_l2"] <= TOL and e["max_rel"] <= TOL, e
 
