@@ -20,6 +20,7 @@
 // plus the score exchange: 80 KiB for D = 256 (two workgroups per CU).
 
 #include <algorithm>
+#include <cstring>
 #include <type_traits>
 #include <utility>
 
@@ -49,6 +50,35 @@ __device__ __forceinline__ f32x16 zero16() {
   return z;
 }
 
+// Arguments of the attention kernels, packed into 112 bytes (launches start about 0.8 us sooner
+// with at most 112 bytes of explicit arguments, as measured for the flash kernels): pointers carry
+// the callers' element offsets, strides are 32-bit (calls with larger strides take the generic
+// kernel), and `o` is the output with one key chunk, the workspace of partial records otherwise.
+struct WideArgs {
+  const float* q;
+  const float* k;
+  const float* v;
+  float* o;
+  const void* mask;   // key lengths (int32) | key mask (uint8)
+  const float* bias;  // dense bias
+  int32_t sq, sk, sv, so;      // batch strides
+  int32_t ldq, ldk, ldv, ldo;  // row strides
+  int32_t Lq, Lk;
+  int32_t sbias, smask;  // dense-bias and key-mask batch strides
+  int32_t tiles;         // workgroups of the launch (the grid size, for the XCD remap)
+  int32_t chunk;         // keys per chunk
+  float scale_log2;
+  int16_t H, nks;        // heads, key chunks per query group
+};
+static_assert(sizeof(WideArgs) == 112, "wide kernel arguments must stay within 112 bytes");
+
+// Arguments of the merge kernel.
+struct MergeArgs {
+  float* o;  // output + its element offset
+  const float* ws;
+  int32_t B, H, Lq, so, ldo, q_groups, nks, nwg;
+};
+
 // Dense bias and key mask of one 32-key block in the 32x32 score layout, where lane (col, half)
 // holds query col's keys k0 + 8(r/4) + 4 half + r%4 in score register r: four runs of 4 keys per
 // lane. Loaded before the block's score products (load), folded into the base-2 scores after them
@@ -68,7 +98,7 @@ struct BlockTerms {
     bool bias_vec, mask_vec;
     int Lk;
   };
-  __device__ static Rows rows(const AttnParams& p, int b, int h, int qi) {
+  __device__ static Rows rows(const WideArgs& p, int b, int h, int qi) {
     Rows r;
     r.Lk = p.Lk;
     r.brow = nullptr;
@@ -81,7 +111,7 @@ struct BlockTerms {
       r.bias_vec = (reinterpret_cast<uintptr_t>(p.bias) & 15) == 0 && (p.Lk & 3) == 0 && (p.sbias & 3) == 0;
     }
     if constexpr (kMask) {
-      r.kmask = p.key_mask + (int64_t)b * p.smask;
+      r.kmask = static_cast<const uint8_t*>(p.mask) + (int64_t)b * p.smask;
       r.mask_vec = (reinterpret_cast<uintptr_t>(r.kmask) & 3) == 0;
     }
     return r;
@@ -121,7 +151,7 @@ struct BlockTerms {
 };
 
 template <int D, int NW, int BIAS, int MASK>
-__global__ __launch_bounds__(64 * NW, 1) void wide_mfma_kernel(AttnParams p, int q_groups, int nks, int chunk, float* ws) {
+__global__ __launch_bounds__(64 * NW, 1) void wide_mfma_kernel(WideArgs p) {
   constexpr int DS = D / NW;      // head dims per wave
   constexpr int QREG = DS / 2;    // Q values per lane
   constexpr int NDB = DS / 32;    // 32-dim output tiles per wave
@@ -143,7 +173,8 @@ __global__ __launch_bounds__(64 * NW, 1) void wide_mfma_kernel(AttnParams p, int
   const int col = lane & 31;
   const int half = lane >> 5;
 
-  int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int q_groups = (p.Lq + 31) >> 5, nks = p.nks, chunk = p.chunk;
+  int tile = xcd_remap(blockIdx.x, p.tiles);
   const int kc = tile % nks;
   tile /= nks;
   const int g = tile % q_groups;
@@ -156,7 +187,7 @@ __global__ __launch_bounds__(64 * NW, 1) void wide_mfma_kernel(AttnParams p, int
   const int slot_base = ((b * p.H + h) * q_groups + g) * nks;
 
   int kv_len = p.Lk;
-  if constexpr (MASK == MASK_KEY_LEN) kv_len = min(max(p.key_len[b], 0), p.Lk);
+  if constexpr (MASK == MASK_KEY_LEN) kv_len = min(max(static_cast<const int32_t*>(p.mask)[b], 0), p.Lk);
   const int kbeg = kc * chunk;
   const int kend = min(kbeg + chunk, kv_len);
   const int nblk = kend > kbeg ? (kend - kbeg + 31) >> 5 : 0;
@@ -166,8 +197,8 @@ __global__ __launch_bounds__(64 * NW, 1) void wide_mfma_kernel(AttnParams p, int
 
   float* const kt = lds_k + wave * SLICE;
   float* const vt = lds_v + wave * SLICE;
-  const float* kbase = p.k + p.k_off + (int64_t)b * p.sk + h * D + wave * DS;
-  const float* vbase = p.v + p.v_off + (int64_t)b * p.sv + h * D + wave * DS;
+  const float* kbase = p.k + (int64_t)b * p.sk + h * D + wave * DS;
+  const float* vbase = p.v + (int64_t)b * p.sv + h * D + wave * DS;
 
   // own K / V slice of block j; rows past the chunk's last key re-read that key
   auto issue_k = [&](int j) {
@@ -201,7 +232,7 @@ __global__ __launch_bounds__(64 * NW, 1) void wide_mfma_kernel(AttnParams p, int
   // Q slice in registers, pre-scaled: lane holds scale*log2(e)*Q[qi][wave*DS + half*DS/2 + s]
   float qr[QREG];
   {
-    const float* src = p.q + p.q_off + (int64_t)b * p.sq + (int64_t)qi * p.ldq + h * D + wave * DS + half * (DS / 2);
+    const float* src = p.q + (int64_t)b * p.sq + (int64_t)qi * p.ldq + h * D + wave * DS + half * (DS / 2);
 #pragma unroll
     for (int i = 0; i < QREG / 4; ++i) {
       f32x4 x = {0.f, 0.f, 0.f, 0.f};
@@ -344,7 +375,7 @@ __global__ __launch_bounds__(64 * NW, 1) void wide_mfma_kernel(AttnParams p, int
   if (nks == 1) {
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
     if (q_valid) {
-      float* dst = p.o + p.o_off + (int64_t)b * p.so + (int64_t)qi * p.ldo + h * D + wave * DS + 4 * half;
+      float* dst = p.o + (int64_t)b * p.so + (int64_t)qi * p.ldo + h * D + wave * DS + 4 * half;
 #pragma unroll
       for (int t = 0; t < NDB; ++t)
 #pragma unroll
@@ -362,7 +393,7 @@ __global__ __launch_bounds__(64 * NW, 1) void wide_mfma_kernel(AttnParams p, int
 
   // ---- publish this chunk's partial: O (unnormalised, relative to m), m, l; the merge kernel
   // combines the chunks of each query group
-  float* rec = ws + (int64_t)(slot_base + kc) * REC;
+  float* rec = p.o + (int64_t)(slot_base + kc) * REC;
   float* orow = rec + col * D + wave * DS + 4 * half;
 #pragma unroll
   for (int t = 0; t < NDB; ++t)
@@ -394,7 +425,7 @@ __global__ __launch_bounds__(64 * NW, 1) void wide_mfma_kernel(AttnParams p, int
 // per SIMD, its loads software-pipelined. Writes the same partial records as wide_mfma_kernel
 // (merged by wide_merge_kernel), staged through LDS into whole-row stores.
 template <int BIAS, int MASK>
-__global__ __launch_bounds__(256, 1) void wide_rows_kernel(AttnParams p, int q_groups, int nks, int chunk, float* ws) {
+__global__ __launch_bounds__(256, 1) void wide_rows_kernel(WideArgs p) {
   constexpr int D = 512;
   constexpr int NG = D / 8;          // groups of 8 head dims (4 MFMAs) per score tile
   constexpr int DS = D / 4;          // output head dims per wave
@@ -413,7 +444,8 @@ __global__ __launch_bounds__(256, 1) void wide_rows_kernel(AttnParams p, int q_g
   const int col = lane & 31;
   const int half = lane >> 5;
 
-  int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int q_groups = (p.Lq + 31) >> 5, nks = p.nks, chunk = p.chunk;
+  int tile = xcd_remap(blockIdx.x, p.tiles);
   const int kc = tile % nks;
   tile /= nks;
   const int g = tile % q_groups;
@@ -424,7 +456,7 @@ __global__ __launch_bounds__(256, 1) void wide_rows_kernel(AttnParams p, int q_g
   const int slot_base = ((b * p.H + h) * q_groups + g) * nks;
 
   int kv_len = p.Lk;
-  if constexpr (MASK == MASK_KEY_LEN) kv_len = min(max(p.key_len[b], 0), p.Lk);
+  if constexpr (MASK == MASK_KEY_LEN) kv_len = min(max(static_cast<const int32_t*>(p.mask)[b], 0), p.Lk);
   const int kbeg = kc * chunk;
   const int kend = min(kbeg + chunk, kv_len);
   const int rounds = kend > kbeg ? (kend - kbeg + 127) >> 7 : 0;
@@ -432,8 +464,8 @@ __global__ __launch_bounds__(256, 1) void wide_rows_kernel(AttnParams p, int q_g
   constexpr bool kTerms = Terms::kBias || Terms::kMask;
   const typename Terms::Rows trows = Terms::rows(p, b, h, q0 + col);
 
-  const float* kbase = p.k + p.k_off + (int64_t)b * p.sk + h * D;
-  const float* vbase = p.v + p.v_off + (int64_t)b * p.sv + h * D + wave * DS;
+  const float* kbase = p.k + (int64_t)b * p.sk + h * D;
+  const float* vbase = p.v + (int64_t)b * p.sv + h * D + wave * DS;
 
   // ---- Q tile (rows past Lq re-read the last row) into registers, then into LDS a quarter of 128
   // head dims at a time as the score products reach it: [quarter][query][32 chunks of 16 bytes],
@@ -442,7 +474,7 @@ __global__ __launch_bounds__(256, 1) void wide_rows_kernel(AttnParams p, int q_g
   // for all of them, and the K loads behind them, before the first LDS read.)
   f32x4 qst[NQ];
   {
-    const float* qbase = p.q + p.q_off + (int64_t)b * p.sq + h * D;
+    const float* qbase = p.q + (int64_t)b * p.sq + h * D;
 #pragma unroll
     for (int n = 0; n < NQ; ++n) {
       const int pc = (n & 3) * 256 + tid;  // physical chunk within quarter n / 4
@@ -645,10 +677,10 @@ __global__ __launch_bounds__(256, 1) void wide_rows_kernel(AttnParams p, int q_g
   float* dst;
   int64_t ld;
   if (nks == 1) {
-    dst = p.o + p.o_off + (int64_t)b * p.so + (int64_t)q0 * p.ldo + h * D + wave * DS;
+    dst = p.o + (int64_t)b * p.so + (int64_t)q0 * p.ldo + h * D + wave * DS;
     ld = p.ldo;
   } else {
-    float* rec = ws + (int64_t)(slot_base + kc) * REC;
+    float* rec = p.o + (int64_t)(slot_base + kc) * REC;
     dst = rec + wave * DS;
     ld = D;
     if (wave == 0 && half == 0) {
@@ -667,10 +699,14 @@ __global__ __launch_bounds__(256, 1) void wide_rows_kernel(AttnParams p, int q_g
 // Combines the nks partial records of every query group: one thread per (query, 4 dims),
 // O = sum_c O_c exp2(m_c - m) / sum_c l_c exp2(m_c - m) with m = max_c m_c (0 if every l_c is 0).
 template <int D>
-__global__ __launch_bounds__(256) void wide_merge_kernel(AttnParams p, int q_groups, int nks, const float* ws) {
+__global__ __launch_bounds__(256) void wide_merge_kernel(MergeArgs p) {
+  const int q_groups = p.q_groups, nks = p.nks;
   constexpr int REC = 32 * D + 64;
   constexpr int C4 = D / 4;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  // the same XCD remap as the attention kernel, whose workgroups wrote a query group's records from
+  // one XCD: consecutive merge workgroups (one query group's queries) run there and find the records
+  // in that XCD's L2
+  const int64_t idx = (int64_t)xcd_remap(blockIdx.x, p.nwg) * 256 + threadIdx.x;
   const int64_t total = (int64_t)p.B * p.H * q_groups * 32 * C4;
   if (idx >= total) return;
   const int d4 = (int)(idx % C4);
@@ -683,7 +719,7 @@ __global__ __launch_bounds__(256) void wide_merge_kernel(AttnParams p, int q_gro
   const int b = bh / p.H;
   const int qi = g * 32 + qq;
   if (qi >= p.Lq) return;
-  const float* recs = ws + r * nks * REC;
+  const float* recs = p.ws + r * nks * REC;
   // One pass over the chunks in groups of 8 whose loads are all issued before any is used
   // (indexes clamped to the last chunk, surplus entries of a group skipped), with a running
   // maximum: the sums so far are rescaled when a group raises it. A query costs ceil(nks/8) load
@@ -729,7 +765,7 @@ __global__ __launch_bounds__(256) void wide_merge_kernel(AttnParams p, int q_gro
   y[1] = acc[1] * inv;
   y[2] = acc[2] * inv;
   y[3] = acc[3] * inv;
-  *reinterpret_cast<f32x4*>(p.o + p.o_off + (int64_t)b * p.so + (int64_t)qi * p.ldo + h * D + 4 * d4) = y;
+  *reinterpret_cast<f32x4*>(p.o + (int64_t)b * p.so + (int64_t)qi * p.ldo + h * D + 4 * d4) = y;
 }
 
 // Waves per workgroup of the head-dim-split kernel (D = 256): each owns D / 4 head dims, 80 KiB of
@@ -739,50 +775,89 @@ template <int D>
 constexpr int kWideWaves = 4;
 
 template <int D, int BIAS, int MASK>
-void launch_main(const AttnParams& p, const WidePlan& plan, float* ws, dim3 grid, hipStream_t stream) {
+void launch_main(const WideArgs& a, dim3 grid, hipStream_t stream) {
   if constexpr (D == 512)
-    hipLaunchKernelGGL((wide_rows_kernel<BIAS, MASK>), grid, dim3(256), 0, stream, p, plan.q_groups, plan.nks,
-                       plan.chunk, ws);
+    hipLaunchKernelGGL((wide_rows_kernel<BIAS, MASK>), grid, dim3(256), 0, stream, a);
   else
-    hipLaunchKernelGGL((wide_mfma_kernel<D, kWideWaves<D>, BIAS, MASK>), grid, dim3(64 * kWideWaves<D>), 0, stream, p,
-                       plan.q_groups, plan.nks, plan.chunk, ws);
+    hipLaunchKernelGGL((wide_mfma_kernel<D, kWideWaves<D>, BIAS, MASK>), grid, dim3(64 * kWideWaves<D>), 0, stream, a);
 }
 
 template <int D, int BIAS>
-hipError_t launch_mask(const AttnParams& p, const WidePlan& plan, float* ws, dim3 grid, hipStream_t stream) {
-  switch (p.mask_mode) {
-    case MASK_NONE: launch_main<D, BIAS, MASK_NONE>(p, plan, ws, grid, stream); break;
-    case MASK_KEY_LEN: launch_main<D, BIAS, MASK_KEY_LEN>(p, plan, ws, grid, stream); break;
-    case MASK_KEY_MASK: launch_main<D, BIAS, MASK_KEY_MASK>(p, plan, ws, grid, stream); break;
+hipError_t launch_mask(const WideArgs& a, int mask_mode, dim3 grid, hipStream_t stream) {
+  switch (mask_mode) {
+    case MASK_NONE: launch_main<D, BIAS, MASK_NONE>(a, grid, stream); break;
+    case MASK_KEY_LEN: launch_main<D, BIAS, MASK_KEY_LEN>(a, grid, stream); break;
+    case MASK_KEY_MASK: launch_main<D, BIAS, MASK_KEY_MASK>(a, grid, stream); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
+bool fits32(int64_t x) { return x >= 0 && x <= 0x7fffffff; }
+
 template <int D>
 hipError_t launch_d(const AttnParams& p, const WidePlan& plan, float* ws, hipStream_t stream) {
   const int64_t n = (int64_t)p.B * p.H * plan.q_groups * plan.nks;
   if (n > 0x7fffffff) return hipErrorInvalidConfiguration;
+  WideArgs a;
+  memset(&a, 0, sizeof a);
+  a.q = p.q + p.q_off;
+  a.k = p.k + p.k_off;
+  a.v = p.v + p.v_off;
+  a.o = plan.nks > 1 ? ws : p.o + p.o_off;
+  a.mask = p.mask_mode == MASK_KEY_LEN ? static_cast<const void*>(p.key_len) : static_cast<const void*>(p.key_mask);
+  a.bias = p.bias;
+  a.sq = (int32_t)p.sq;
+  a.sk = (int32_t)p.sk;
+  a.sv = (int32_t)p.sv;
+  a.so = (int32_t)p.so;
+  a.ldq = (int32_t)p.ldq;
+  a.ldk = (int32_t)p.ldk;
+  a.ldv = (int32_t)p.ldv;
+  a.ldo = (int32_t)p.ldo;
+  a.Lq = p.Lq;
+  a.Lk = p.Lk;
+  a.sbias = (int32_t)p.sbias;
+  a.smask = (int32_t)p.smask;
+  a.tiles = (int32_t)n;
+  a.chunk = plan.chunk;
+  a.scale_log2 = p.scale_log2;
+  a.H = (int16_t)p.H;
+  a.nks = (int16_t)plan.nks;
   const dim3 grid((unsigned)n);
   hipError_t e;
   if (p.bias_mode == BIAS_NONE)
-    e = launch_mask<D, BIAS_NONE>(p, plan, ws, grid, stream);
+    e = launch_mask<D, BIAS_NONE>(a, p.mask_mode, grid, stream);
   else if (p.bias_mode == BIAS_DENSE)
-    e = launch_mask<D, BIAS_DENSE>(p, plan, ws, grid, stream);
+    e = launch_mask<D, BIAS_DENSE>(a, p.mask_mode, grid, stream);
   else
     return hipErrorInvalidValue;
   if (e != hipSuccess || plan.nks == 1) return e;
   const int64_t threads = (int64_t)p.B * p.H * plan.q_groups * 32 * (D / 4);
   const int64_t blocks = (threads + 255) / 256;
   if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((wide_merge_kernel<D>), dim3((unsigned)blocks), dim3(256), 0, stream, p, plan.q_groups, plan.nks, ws);
+  MergeArgs m;
+  m.o = p.o + p.o_off;
+  m.ws = ws;
+  m.B = p.B;
+  m.H = p.H;
+  m.Lq = p.Lq;
+  m.so = (int32_t)p.so;
+  m.ldo = (int32_t)p.ldo;
+  m.q_groups = plan.q_groups;
+  m.nks = plan.nks;
+  m.nwg = (int32_t)blocks;
+  hipLaunchKernelGGL((wide_merge_kernel<D>), dim3((unsigned)blocks), dim3(256), 0, stream, m);
   return hipGetLastError();
 }
 
 }  // namespace
 
 bool wide_mfma_supported(const AttnParams& p) {
-  return (p.D == 256 || p.D == 512) && (p.bias_mode == BIAS_NONE || p.bias_mode == BIAS_DENSE) &&
+  // 32-bit strides and at most 32767 heads (the packed arguments); other calls take the generic kernel
+  const bool fit = fits32(p.sq) && fits32(p.sk) && fits32(p.sv) && fits32(p.so) && fits32(p.ldq) && fits32(p.ldk) &&
+                   fits32(p.ldv) && fits32(p.ldo) && fits32(p.sbias) && fits32(p.smask) && p.H <= 32767;
+  return fit && (p.D == 256 || p.D == 512) && (p.bias_mode == BIAS_NONE || p.bias_mode == BIAS_DENSE) &&
          (p.mask_mode == MASK_NONE || p.mask_mode == MASK_KEY_LEN || p.mask_mode == MASK_KEY_MASK);
 }
 
