@@ -42,6 +42,8 @@
 #include <algorithm>
 #include <type_traits>
 
+#include <cstring>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -84,6 +86,23 @@ struct TileOrder {
   int tiles_m, tiles_n, group_n, sb_rows;
 };
 
+// Arguments of the MFMA kernels: 80 bytes, 96 with the tile order (launches with at most 112 bytes
+// of explicit arguments start sooner). Pointers carry the callers' element offsets, resid is the
+// residual rows (y itself when the caller gave none), and the row strides fit 32 bits under
+// linear_mfma_supported.
+struct LinArgs {
+  const float* x;
+  const float* w;
+  const float* bias;
+  const float* gate;
+  float* y;
+  const float* resid;
+  int32_t ldx, ldw, ldy;
+  int32_t M, N, K;
+  float alpha;
+};
+static_assert(sizeof(LinArgs) + sizeof(TileOrder) <= 112, "linear kernel arguments must stay within 112 bytes");
+
 __device__ __forceinline__ void tile_coords(int t, const TileOrder& o, int& mi, int& ni) {
   const int sb_tiles = o.sb_rows * o.tiles_n;
   const int sb = t / sb_tiles;
@@ -99,7 +118,7 @@ __device__ __forceinline__ void tile_coords(int t, const TileOrder& o, int& mi, 
 // WM x WN accumulators per wave, BK k per tile (16 or 32), NS tiles in flight (LDS stages); the
 // activation and the epilogue are compile-time, so the store loop has no per-element branches.
 template <int WM, int WN, int BK, int NS, int ACT, int EPI>
-__global__ __launch_bounds__(256, 2) void linear_mfma_kernel(LinearParams p, TileOrder order) {
+__global__ __launch_bounds__(256, 2) void linear_mfma_kernel(LinArgs p, TileOrder order) {
   constexpr int BM = 64 * WM;
   constexpr int BN = 64 * WN;
   constexpr int CPR = BK / 4;            // 16-byte chunks per tile row
@@ -130,7 +149,7 @@ __global__ __launch_bounds__(256, 2) void linear_mfma_kernel(LinearParams p, Til
   const int m0 = mi * BM;
   const int n0 = ni * BN;
 
-  const float* xbase = p.x + p.x_off + (int64_t)m0 * p.ldx;
+  const float* xbase = p.x + (int64_t)m0 * p.ldx;
   const float* wbase = p.w + (int64_t)n0 * p.ldw;
   const int mlast = min(BM, p.M - m0) - 1;  // last valid tile row
   const int nlast = min(BN, p.N - n0) - 1;
@@ -287,8 +306,8 @@ __global__ __launch_bounds__(256, 2) void linear_mfma_kernel(LinearParams p, Til
   const int nw = n0 + wn * 32 * WN;
   const bool full = m0 + BM <= p.M && n0 + BN <= p.N;
   const __amdgpu_buffer_rsrc_t yr =
-      __builtin_amdgcn_make_buffer_rsrc(p.y + p.y_off + (int64_t)mw * p.ldy + nw, 0, 0x7fffffff, 0x00020000);
-  const float* rsrc_base = (p.resid ? p.resid : p.y) + p.y_off + (int64_t)mw * p.ldy + nw;  // residual rows
+      __builtin_amdgcn_make_buffer_rsrc(p.y + (int64_t)mw * p.ldy + nw, 0, 0x7fffffff, 0x00020000);
+  const float* rsrc_base = p.resid + (int64_t)mw * p.ldy + nw;  // residual rows
   const __amdgpu_buffer_rsrc_t rr_ = buffer_rsrc(rsrc_base);
   const int ldy4 = 4 * (int)p.ldy;
   // Plain stores are non-temporal (cache policy NT): y is not read back here, and keeping it out of
@@ -303,7 +322,7 @@ __global__ __launch_bounds__(256, 2) void linear_mfma_kernel(LinearParams p, Til
       const bool n_ok = !kCheck || nw + nl < p.N;
       const float bias_n = (p.bias && n_ok) ? p.bias[nw + nl] : 0.f;
       float gate_n = 1.f;
-      if constexpr (EPI == LIN_EPI_RESID_GATE) gate_n = n_ok ? p.gate[p.gate_off + nw + nl] : 0.f;
+      if constexpr (EPI == LIN_EPI_RESID_GATE) gate_n = n_ok ? p.gate[nw + nl] : 0.f;
 #pragma unroll
       for (int i = 0; i < WM; ++i) {
         const int voff = (32 * i + 4 * half) * ldy4 + 4 * nl;
@@ -345,7 +364,7 @@ __global__ __launch_bounds__(256, 2) void linear_mfma_kernel(LinearParams p, Til
 // order) for 16/KS of its accumulator registers each and run the epilogue for those rows. Copies,
 // swizzle and the clamped last k-tile as in linear_mfma_kernel.
 template <int TM, int TN, int KS, int ACT, int EPI>
-__global__ __launch_bounds__(64 * TM * TN * KS) void linear_ksplit_kernel(LinearParams p, TileOrder order) {
+__global__ __launch_bounds__(64 * TM * TN * KS) void linear_ksplit_kernel(LinArgs p, TileOrder order) {
   constexpr int BM = 32 * TM, BN = 32 * TN, BK = 64, NS = 2;
   constexpr int NWAVE = TM * TN * KS;
   constexpr int NT = 64 * NWAVE;     // threads
@@ -398,7 +417,7 @@ __global__ __launch_bounds__(64 * TM * TN * KS) void linear_ksplit_kernel(Linear
     bcol[n] = 4 * c;
     boff[n] = 4u * (unsigned)(min(row, nlast) * (int)p.ldw + 4 * c);
   }
-  const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(p.x + p.x_off + (int64_t)m0 * p.ldx);
+  const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(p.x + (int64_t)m0 * p.ldx);
   const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(p.w + (int64_t)n0 * p.ldw);
   const int nkt = (p.K + BK - 1) / BK;
   const int nfull = p.K / BK;
@@ -468,8 +487,8 @@ __global__ __launch_bounds__(64 * TM * TN * KS) void linear_ksplit_kernel(Linear
   if (n >= p.N) return;
   const float bias_n = p.bias ? p.bias[n] : 0.f;
   float gate_n = 1.f;
-  if constexpr (EPI == LIN_EPI_RESID_GATE) gate_n = p.gate[p.gate_off + n];
-  const float* rsrc = p.resid ? p.resid : p.y;
+  if constexpr (EPI == LIN_EPI_RESID_GATE) gate_n = p.gate[n];
+  const float* rsrc = p.resid;
 #pragma unroll
   for (int k = 0; k < RPW; ++k) {
     const int r = RPW * ks + k;
@@ -479,7 +498,7 @@ __global__ __launch_bounds__(64 * TM * TN * KS) void linear_ksplit_kernel(Linear
 #pragma unroll
       for (int w = 1; w < KS; ++w) sum += red[((w * TM * TN + blk) * 16 + r) * 64 + lane];
       float v = apply_act<ACT>(fmaf(sum, p.alpha, bias_n));
-      const int64_t e = p.y_off + (int64_t)m * p.ldy + n;
+      const int64_t e = (int64_t)m * p.ldy + n;
       if constexpr (EPI != LIN_EPI_STORE) v = fmaf(gate_n, v, rsrc[e]);
       if constexpr (EPI == LIN_EPI_STORE) {
         __builtin_nontemporal_store(v, p.y + e);  // not read back here, as in linear_mfma_kernel
@@ -550,13 +569,32 @@ TileOrder tile_order(const LinearParams& p, int bm, int bn) {
   return o;
 }
 
+LinArgs lin_args(const LinearParams& p) {
+  LinArgs a;
+  memset(&a, 0, sizeof a);
+  a.x = p.x + p.x_off;
+  a.w = p.w;
+  a.bias = p.bias;
+  a.gate = p.gate ? p.gate + p.gate_off : nullptr;
+  a.y = p.y + p.y_off;
+  a.resid = (p.resid ? p.resid : p.y) + p.y_off;
+  a.ldx = (int32_t)p.ldx;
+  a.ldw = (int32_t)p.ldw;
+  a.ldy = (int32_t)p.ldy;
+  a.M = p.M;
+  a.N = p.N;
+  a.K = p.K;
+  a.alpha = p.alpha;
+  return a;
+}
+
 template <int WM, int WN, int BK, int NS, int ACT, int EPI>
 hipError_t launch_tiles(const LinearParams& p, hipStream_t stream) {
   const int64_t tm = (p.M + 64 * WM - 1) / (64 * WM);
   const int64_t tn = (p.N + 64 * WN - 1) / (64 * WN);
   if (tm * tn > 0x7fffffff) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((linear_mfma_kernel<WM, WN, BK, NS, ACT, EPI>), dim3((unsigned)(tm * tn)), dim3(256), 0, stream, p,
-                     tile_order(p, 64 * WM, 64 * WN));
+  hipLaunchKernelGGL((linear_mfma_kernel<WM, WN, BK, NS, ACT, EPI>), dim3((unsigned)(tm * tn)), dim3(256), 0, stream,
+                     lin_args(p), tile_order(p, 64 * WM, 64 * WN));
   return hipGetLastError();
 }
 
@@ -580,7 +618,7 @@ hipError_t launch_ksplit_tiles(const LinearParams& p, hipStream_t stream) {
   const int64_t n = (int64_t)o.tiles_m * o.tiles_n;
   if (n > 0x7fffffff) return hipErrorInvalidConfiguration;
   hipLaunchKernelGGL((linear_ksplit_kernel<TM, TN, KS, ACT, EPI>), dim3((unsigned)n), dim3(64 * TM * TN * KS), 0, stream,
-                     p, o);
+                     lin_args(p), o);
   return hipGetLastError();
 }
 
@@ -622,6 +660,7 @@ bool linear_mfma_supported(const LinearParams& p) {
   auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
   // copies address a tile's rows as 32-bit byte offsets from its first row (up to 128 x rows and
   // 192 W rows, plus the k offset <= the row stride); stores address up to 128 output rows likewise
+  // (the same bounds keep the row strides within the 32 bits of the kernels' arguments)
   return p.K % 8 == 0 && a16(p.x) && a16(p.w) && p.x_off % 4 == 0 && p.ldx % 4 == 0 && p.ldw % 4 == 0 &&
          (int64_t)(64 * 2 + 1) * p.ldx * 4 < 0x7fffffffLL && (int64_t)(64 * 3 + 1) * p.ldw * 4 < 0x7fffffffLL &&
          (int64_t)64 * 2 * p.ldy * 4 < 0x7fffffffLL;
