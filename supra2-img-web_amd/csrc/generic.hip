@@ -127,9 +127,9 @@ __global__ __launch_bounds__(kThreads) void generic_kernel(AttnParams p) {
   }
 }
 
-__global__ void position_bias_kernel(const float* table, const int32_t* lut, int num_buckets, int H, int Lq,
+__global__ __launch_bounds__(256) void position_bias_kernel(const float* table, const int32_t* lut, int num_buckets, int H, int Lq,
                                      int Lk, float* out, int64_t n) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // launched with 256 threads (no blockDim read)
   if (idx >= n) return;
   const int j = (int)(idx % Lk);
   const int64_t r = idx / Lk;

@@ -123,14 +123,14 @@ __device__ __forceinline__ void load_quad(const typename Raw<DT>::T* p, typename
 // dst[i] = decode(src[i]) for i < n. Elements [0, head) and [head + 4*quads, n) one per thread;
 // the middle as quads: lane j of a pass writes output float4 j, so every store instruction of a
 // wave covers 1 KiB of whole lines (dst + head is 16-byte aligned), and every load instruction
-// reads the matching contiguous source bytes.
+// reads the matching contiguous source bytes. nthreads: the grid's threads, an argument rather than
+// gridDim (reading the grid size makes the runtime pass its hidden arguments, and launches start later).
 template <int DT, bool VEC>
 __global__ __launch_bounds__(kThreads) void to_f32_kernel(const uint8_t* __restrict__ src, float* __restrict__ dst,
-                                                          int64_t n, int64_t head, int64_t quads) {
+                                                          int64_t n, int64_t head, int64_t quads, int64_t nthreads) {
   using T = typename Raw<DT>::T;
   constexpr int U = kQuadsPerThread<DT>;
   const int64_t tid = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  const int64_t nthreads = (int64_t)gridDim.x * kThreads;
   const T* s = reinterpret_cast<const T*>(src);
   const int64_t tail0 = head + quads * 4;
   for (int64_t i = tid; i < head; i += nthreads) dst[i] = decode<DT>(s[i]);
@@ -156,9 +156,8 @@ __global__ __launch_bounds__(kThreads) void to_f32_kernel(const uint8_t* __restr
 // Any source alignment: every element assembled from bytes.
 template <int DT>
 __global__ __launch_bounds__(kThreads) void to_f32_bytes_kernel(const uint8_t* __restrict__ src, float* __restrict__ dst,
-                                                                int64_t n) {
+                                                                int64_t n, int64_t nthreads) {
   using T = typename Raw<DT>::T;
-  const int64_t nthreads = (int64_t)gridDim.x * kThreads;
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += nthreads)
     dst[i] = decode<DT>(load_bytes<DT>(src + i * (int64_t)sizeof(T)));
 }
@@ -214,7 +213,8 @@ template <int DT>
 hipError_t launch_to_f32(const uint8_t* src, float* dst, int64_t n, hipStream_t stream) {
   using T = typename Raw<DT>::T;
   if ((uintptr_t)src % sizeof(T) != 0) {
-    hipLaunchKernelGGL(to_f32_bytes_kernel<DT>, dim3(grid_for(n)), dim3(kThreads), 0, stream, src, dst, n);
+    const unsigned g = grid_for(n);
+    hipLaunchKernelGGL(to_f32_bytes_kernel<DT>, dim3(g), dim3(kThreads), 0, stream, src, dst, n, (int64_t)g * kThreads);
     return hipGetLastError();
   }
   int64_t head = (int64_t)((16 - (uintptr_t)dst % 16) % 16) / 4;  // dst + head is 16-byte aligned
@@ -228,8 +228,13 @@ hipError_t launch_to_f32(const uint8_t* src, float* dst, int64_t n, hipStream_t 
   int64_t blocks = (threads + kThreads - 1) / kThreads;
   if (blocks < 1) blocks = 1;
   if (blocks > (1 << 30)) blocks = 1 << 30;  // the loops stride over the rest
-  if (vec) hipLaunchKernelGGL((to_f32_kernel<DT, true>), dim3((unsigned)blocks), dim3(kThreads), 0, stream, src, dst, n, head, quads);
-  else hipLaunchKernelGGL((to_f32_kernel<DT, false>), dim3((unsigned)blocks), dim3(kThreads), 0, stream, src, dst, n, head, quads);
+  const int64_t nthreads = (int64_t)blocks * kThreads;
+  if (vec)
+    hipLaunchKernelGGL((to_f32_kernel<DT, true>), dim3((unsigned)blocks), dim3(kThreads), 0, stream, src, dst, n, head, quads,
+                       nthreads);
+  else
+    hipLaunchKernelGGL((to_f32_kernel<DT, false>), dim3((unsigned)blocks), dim3(kThreads), 0, stream, src, dst, n, head,
+                       quads, nthreads);
   return hipGetLastError();
 }
 
