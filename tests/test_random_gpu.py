@@ -9,7 +9,9 @@ element offsets, output row padding, scales of either sign, dense and relative-p
 per-sequence key lengths (zero included) and boolean key masks. Linear calls cover the 64 x 64 MFMA
 tile and the generic kernel (the large-grid tiles are exercised at full scale in test_linear_gpu.py),
 ragged M/N/K, strides and offsets on every operand, alpha, the four activations and the three
-epilogues. Sizes keep the float64 oracle to a few seconds in total.
+epilogues. A second seeded draw adds wide-head calls with dense biases and key lengths or masks, and
+head-dim-64 small launches whose short sequences pack (with the host copy of the key lengths). Sizes
+keep the float64 oracle to a few seconds in total.
 """
 
 from __future__ import annotations
@@ -91,7 +93,53 @@ def _linear_cases(seed: int, n: int) -> list[dict]:
     return cases
 
 
+def _wide_and_packed_cases(seed: int, n: int) -> list[dict]:
+    """Half wide-head calls (D 256 / 512) with dense biases and either mask kind, half head-dim-64 small
+    launches whose key lengths (many of at most 64 keys, with the host copy) pack their sequences."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        if i % 2 == 0:
+            D = int(rng.choice([256, 512]))
+            B, H = int(rng.integers(1, 4)), int(rng.integers(1, 3))
+            Lq, Lk = int(rng.integers(1, 300)), int(rng.integers(1, 300))
+            while B * H * Lq * Lk * D > OPS_BUDGET:
+                Lq, Lk = max(1, Lq // 2), max(1, Lk // 2)
+            kw = dict(B=B, H=H, D=D, Lq=Lq, Lk=Lk, seed=3000 + i, pad_cols=int(rng.choice([0, 4, 8])),
+                      o_off=int(rng.choice([0, 8])), ldo_pad=int(rng.choice([0, 4])))
+            if rng.random() < 0.7:
+                kw["bias_mode"] = _lib.SA_BIAS_DENSE
+                kw["dense_bias_batched"] = bool(rng.random() < 0.5)
+            r = rng.random()
+            if r < 0.4:
+                kw["mask_mode"] = _lib.SA_MASK_KEY_LEN
+                kw["key_len"] = [int(x) for x in rng.integers(0, Lk + 1, size=B)]
+            elif r < 0.8:
+                kw["mask_mode"] = _lib.SA_MASK_KEY_MASK
+                kw["key_mask_p"] = float(rng.choice([0.1, 0.5, 0.9]))
+        else:
+            B = int(rng.integers(2, 17))
+            H = int(rng.integers(1, max(2, min(13, 128 // B + 1))))
+            Lk = int(rng.integers(96, 200))
+            # more 16-query groups than the 256 CUs, at most 256 groups of 32 (the small-launch range):
+            # with a = 256 // (B * H), exactly Lq in [16a + 1, 32a]
+            a = 256 // (B * H)
+            Lq = int(rng.integers(16 * a + 1, 32 * a + 1))
+            kl = rng.integers(0, 65, size=B)
+            long_ = rng.random(B) < 0.4
+            kl[long_] = rng.integers(65, Lk + 1, size=int(long_.sum()))
+            kw = dict(B=B, H=H, D=64, Lq=Lq, Lk=Lk, seed=3000 + i, mask_mode=_lib.SA_MASK_KEY_LEN,
+                      key_len=[int(x) for x in kl], bias_mode=int(rng.choice([0, 1, 2])))
+            if kw["bias_mode"] == _lib.SA_BIAS_RELPOS:
+                kw["scale"] = 1.0 / 8.0
+        kw["name"] = (f"rand_wp{i}_B{kw['B']}H{kw['H']}D{kw['D']}q{kw['Lq']}k{kw['Lk']}"
+                      f"_b{kw.get('bias_mode', 0)}m{kw.get('mask_mode', 0)}")
+        cases.append(kw)
+    return cases
+
+
 ATTENTION = _attention_cases(seed=2026, n=40)
+WIDE_PACKED = _wide_and_packed_cases(seed=2028, n=24)
 LINEAR = _linear_cases(seed=2027, n=24)
 
 
@@ -119,6 +167,32 @@ def test_draw_reaches_every_kernel():
         names.add(_lib.kernel_name(args).split("_split")[0])
     assert {"flash_mfma_d64", "flash_mfma_d128", "generic"} <= names, names
     assert any(n.startswith("wide") for n in names) and any(n.startswith("flash_small") for n in names), names
+
+
+@pytest.mark.parametrize("case", WIDE_PACKED, ids=[c["name"] for c in WIDE_PACKED])
+def test_random_wide_and_packed(dev, case):
+    kw = dict(case)
+    key_len = kw.pop("key_len", None)
+    call = make_call(key_len=key_len, **kw)
+    run_attention(dev, call, check_fp64=call.B * call.H * call.Lq * call.Lk * call.D <= 4_000_000)
+
+
+def test_wide_and_packed_draw_reaches_its_variants():
+    """The second draw reaches the wide kernels with a dense bias under both mask kinds and the packed
+    small-launch variant (host only, with the host copy of the key lengths as the GPU run passes it)."""
+    from variant_cases import fake_args
+
+    variants = set()
+    for case in WIDE_PACKED:
+        kw = dict(case)
+        key_len = kw.pop("key_len", None)
+        call = make_call(key_len=key_len, **kw)
+        variants.add(_lib.plan(fake_args(call, True)).variant())
+    wide = {(v[1], v[3], v[4]) for v in variants if v[0] == _lib.SA_KERNEL_WIDE}
+    assert {(d, _lib.SA_BIAS_DENSE, _lib.SA_MASK_KEY_LEN) for d in (256, 512)} & wide, wide
+    assert {(d, _lib.SA_BIAS_DENSE, _lib.SA_MASK_KEY_MASK) for d in (256, 512)} & wide, wide
+    packed = [v for v in variants if v[0] == _lib.SA_KERNEL_FLASH_SMALL16 and v[4] == 3]
+    assert len({v[3] for v in packed}) >= 2, variants
 
 
 @pytest.mark.parametrize("case", LINEAR, ids=[c["name"] for c in LINEAR])
