@@ -163,6 +163,10 @@ def test_generic_kernel_for_other_head_dims_and_unaligned_rows():
     assert _lib.kernel_name(good_args(**wide, mask_mode=2, key_mask=FAKE + (2 << 32))) == "wide_mfma_d512"
     assert _lib.kernel_name(good_args(**wide, bias_mode=2, bias=FAKE + (2 << 32), bucket_lut=FAKE + (3 << 32),
                                       num_buckets=32)) == "generic"
+    # the wide kernels take 32-bit strides: a batch stride past 2^31 - 1 elements takes the generic kernel
+    far = dict(wide, so=1 << 31, o=FAKE + (1 << 44))
+    assert _lib.kernel_name(good_args(**far)) == "generic"
+    assert _lib.kernel_name(good_args(**dict(far, so=(1 << 31) - 1024))) == "wide_mfma_d512"
 
 
 @pytest.mark.parametrize("over,code", [
@@ -410,6 +414,10 @@ def test_linear_kernel_choice():
     assert _lib.linear_kernel_name(lin_args(x_off=1)) == "linear_generic"         # unaligned rows
     assert _lib.linear_kernel_name(lin_args(x=FAKE + 4)) == "linear_generic"
     assert _lib.linear_kernel_name(lin_args(ldw=578)) == "linear_generic"
+    # the MFMA kernels take 32-bit row strides: row offsets of a 128-row x tile past 2^31 bytes take the
+    # generic kernel (which keeps 64-bit strides)
+    assert _lib.linear_kernel_name(lin_args(ldx=1 << 22, M=64)) == "linear_generic"
+    assert _lib.linear_kernel_name(lin_args(ldy=1 << 22, M=64, y=FAKE + (1 << 44))) == "linear_generic"
 
 
 @pytest.mark.parametrize("over,code", [
