@@ -77,7 +77,8 @@ function crossAttention(gpu, q, ctx, opts) {
   return ops.attention(gpu, {
     B: ctx.B, q: q, k: ctx.kv, v: ctx.kv, Lq: c.T, Lk: ctx.Lmax, H: c.H, D: c.D, ldq: c.dim, ldk: ldkv, ldv: ldkv,
     qOff: 0, kOff: 0, vOff: c.dim, sq: c.T * c.dim, sk: ctx.Lmax * ldkv, sv: ctx.Lmax * ldkv, so: c.T * c.dim,
-    keyLen: ctx.keyLen, keyLenHost: ctx.lens, out: c.out,  // host lengths: balanced schedule
+    // host lengths: the flash kernel's balanced schedule, or short sequences packed in small launches
+    keyLen: ctx.keyLen, keyLenHost: ctx.lens, out: c.out,
   });
 }
 

@@ -42,6 +42,11 @@ def test_reference_call_forms_through_node(tmp_path):
                   "q": _save(d, "cq.bin", c.q),
                   "kv": [_save(d, "kv0.bin", kv[0, :77]), _save(d, "kv1.bin", kv[1, :1])]})
     refs["dit_cross_loop"] = orc.reference_torch(c).reshape(2 * 256, 576)
+    # the guided batch of two through the batched call site: its one-key sequence is packed into fewer
+    # workgroups of the 16-query small-launch kernel (the host lengths travel with the call)
+    cases.append({"name": "dit_cross_callsite_b2", "form": "dit_cross_callsite", "B": 2, "L": [77, 1],
+                  "q": cases[-1]["q"], "kv": cases[-1]["kv"]})
+    refs["dit_cross_callsite_b2"] = refs["dit_cross_loop"]
 
     s4 = workloads.dit_self(B=4, seed=14)
     cases.append({"name": "dit_self_callsite", "form": "dit_self_callsite", "B": 4, "qkv": _save(d, "qkv4.bin", s4.q)})
