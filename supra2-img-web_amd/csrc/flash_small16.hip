@@ -439,14 +439,23 @@ bool small16_packing(const AttnParams& p, uint32_t* code) {
   return packs;
 }
 
+// The grid of a launch and whether (with which codes) it packs, from one read of the host lengths:
+// the kernel's workgroup decode relies on the grid being exactly the codes' workgroups.
+int64_t small16_grid(const AttnParams& p, uint32_t* code, bool* packed) {
+  *code = 0;
+  *packed = small16_packing(p, code);
+  if (!*packed) return (int64_t)p.B * p.H * ((p.Lq + kQG - 1) / kQG);
+  int lw[kMaxPacked];
+  for (int s = 0; s < p.B; ++s) lw[s] = (*code >> (2 * s)) & 3;
+  return packed_workgroups(p, lw);
+}
+
 }  // namespace
 
 int64_t flash_small16_workgroups(const AttnParams& p) {
-  uint32_t code = 0;
-  if (!small16_packing(p, &code)) return (int64_t)p.B * p.H * ((p.Lq + kQG - 1) / kQG);
-  int lw[kMaxPacked];
-  for (int s = 0; s < p.B; ++s) lw[s] = (code >> (2 * s)) & 3;
-  return packed_workgroups(p, lw);
+  uint32_t code;
+  bool packed;
+  return small16_grid(p, &code, &packed);
 }
 
 FlashVariant flash_small16_variant(const AttnParams& p) {
@@ -467,12 +476,13 @@ int flash_small16_variants(FlashVariant* out, int cap) {
 }
 
 hipError_t launch_flash_small16(const AttnParams& p, hipStream_t stream) {
-  const int64_t n = flash_small16_workgroups(p);
+  uint32_t code;
+  bool packed;
+  const int64_t n = small16_grid(p, &code, &packed);
   if (p.D != kD || n > 0x7fffffff || !flash_mfma_args_fit(p)) return hipErrorInvalidValue;
   FlashArgs a = flash_args(p, n);  // aux: the key-mask row stride (key-mask calls), the packing codes
-  uint32_t code = 0;
   int mask = p.mask_mode;
-  if (small16_packing(p, &code)) {
+  if (packed) {
     mask = MASK_KEY_LEN_ORDERED;
     a.aux = (int32_t)code;
   }
