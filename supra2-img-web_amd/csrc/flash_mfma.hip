@@ -311,14 +311,44 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
         for (int i = 0; i < QREG / 4; ++i)
           kpre[i] = *reinterpret_cast<const f32x4*>(krow + 4 * ((2 * i + half) ^ ksw));
       }
+      // Key-length masks, a block with at most 16 valid keys (the last block of a sequence): its scores
+      // for keys 0..15 only, as four 16x16 blocks of v_mfma_f32_16x16x1f32 at half the cycles of the
+      // 32x32x2 chain. Block b takes its operands from lanes 16b..16b+15: query half b & 1 and head-dim
+      // half b >> 1, i.e. each lane's own query (col) and its own Q registers, with K row col & 15.
+      // The two head-dim halves are summed in-lane (block b's result sits in registers 4b..4b+3, row
+      // 4(l/16) + r, column l % 16), and one v_permlane16_swap and one v_permlane32_swap per register
+      // pair move keys 4h + r and 8 + 4h + r of query col to registers r and 4 + r of the 32x32 layout
+      // (h = half); registers 8..15 (keys 16..31) are masked below.
+      constexpr bool kShortScores = MASK == MASK_KEY_LEN || MASK == MASK_KEY_LEN_ORDERED;
+      if (kShortScores && kv_len - k0 <= 16) {
+        const float* krow16 = kt + (ks * 32 + (col & 15)) * D;
 #pragma unroll
-      for (int i = 0; i < QREG / 4; ++i) {
-        const int c = (2 * i + half) ^ ksw;
-        const f32x4 kv = kPrefetch ? kpre[i] : *reinterpret_cast<const f32x4*>(krow + 4 * c);
-        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[0], qr[4 * i + 0], s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[1], qr[4 * i + 1], s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[2], qr[4 * i + 2], s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[3], qr[4 * i + 3], s, 0, 0, 0);
+        for (int i = 0; i < QREG / 4; ++i) {
+          const f32x4 kv = *reinterpret_cast<const f32x4*>(krow16 + 4 * ((2 * i + half) ^ ksw));
+          s = __builtin_amdgcn_mfma_f32_16x16x1f32(kv[0], qr[4 * i + 0], s, 0, 0, 0);
+          s = __builtin_amdgcn_mfma_f32_16x16x1f32(kv[1], qr[4 * i + 1], s, 0, 0, 0);
+          s = __builtin_amdgcn_mfma_f32_16x16x1f32(kv[2], qr[4 * i + 2], s, 0, 0, 0);
+          s = __builtin_amdgcn_mfma_f32_16x16x1f32(kv[3], qr[4 * i + 3], s, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float x = s[r] + s[8 + r];       // query half 0
+          const float y = s[4 + r] + s[12 + r];  // query half 1
+          const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+          const auto z = __builtin_amdgcn_permlane32_swap(a[0], a[1], false, false);
+          s[r] = __uint_as_float(z[0]);
+          s[4 + r] = __uint_as_float(z[1]);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < QREG / 4; ++i) {
+          const int c = (2 * i + half) ^ ksw;
+          const f32x4 kv = kPrefetch ? kpre[i] : *reinterpret_cast<const f32x4*>(krow + 4 * c);
+          s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[0], qr[4 * i + 0], s, 0, 0, 0);
+          s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[1], qr[4 * i + 1], s, 0, 0, 0);
+          s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[2], qr[4 * i + 2], s, 0, 0, 0);
+          s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[3], qr[4 * i + 3], s, 0, 0, 0);
+        }
       }
       // likewise the V operands of the PV step (head dim 64), read while the softmax runs
       constexpr bool vPrefetch = NSPLIT > 1 && D == 64;
