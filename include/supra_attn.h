@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SA_ABI_VERSION 4
+#define SA_ABI_VERSION 5
 
 /* ---- status codes ---- */
 #define SA_OK 0
@@ -184,10 +184,12 @@ typedef struct sa_attn_plan {
   int64_t workspace_bytes; /* sa_attention_workspace_bytes(args) */
   const char* name;        /* sa_attention_kernel_name(args) (static storage) */
   /* FLASH launches of more units (query tiles) than fit the GPU at once whose last round holds
-   * few units: those last units run in a second launch at one workgroup per CU, of the
+   * few units: those last units run at one workgroup per CU, in a second launch of the
    * small-launch kernel (tail_kernel SA_KERNEL_FLASH_SMALL, tail_key_split 4 waves per 32 queries)
-   * or of the flash kernel split by keys over 2 waves per 32 queries (SA_KERNEL_FLASH, 2);
-   * tail_kernel is 0 when there is no second launch, tail_workgroups the second launch's grid. */
+   * or of the flash kernel split by keys over 2 waves per 32 queries (SA_KERNEL_FLASH, 2), or, when
+   * tail_folded is 1, as 64-query units of the latter run inside the first launch (see tail_folded);
+   * tail_kernel is 0 when there are no such units, tail_workgroups the number of workgroups (or, folded,
+   * of 64-query units) they take. */
   int32_t tail_kernel;
   int32_t tail_key_split;
   int64_t tail_workgroups;
@@ -198,11 +200,17 @@ typedef struct sa_attn_plan {
    * B; otherwise order_n is 0 and sequence_order all zero. */
   int32_t order_n;
   uint8_t sequence_order[256];
+  /* Revision 3 (appended: revision-1 and revision-2 structs are still accepted, without it). 1 when
+   * the units past the first round run inside the first launch: a launch of one round plus at most
+   * half a round, whose first tail_workgroups workgroups (the first one on each CU) each run one
+   * 64-query unit of them, split by keys over 2 waves per 32 queries, after their own unit; 0 otherwise. */
+  int32_t tail_folded;
 } sa_attn_plan;
 
 /* Fills *plan for these arguments: SA_OK, or the status sa_attention_f32 would return for a
  * rejected call (nothing is launched either way). plan->struct_size: sizeof(sa_attn_plan), or the
- * revision-1 size (offsetof(sa_attn_plan, order_n)). Host only. */
+ * revision-2 size (offsetof(sa_attn_plan, tail_folded)) or the revision-1 size
+ * (offsetof(sa_attn_plan, order_n)). Host only. */
 int sa_attention_plan(const sa_attn_args* args, sa_attn_plan* plan);
 
 /* Number of compiled kernel variants; sa_attention_variant(i, plan) describes variant i

@@ -91,8 +91,11 @@ bool too_large(int64_t v) { return v >= kMaxExtent; }
 
 // Size of the revision-2 struct (it ended at workspace_bytes); still accepted.
 constexpr uint32_t kAttnArgsV2Size = offsetof(sa_attn_args, key_len_host);
-// Size of the revision-1 sa_attn_plan (it ended at tail_workgroups); still accepted.
+// Sizes of the revision-1 sa_attn_plan (it ended at tail_workgroups) and of revision 2 (it ended at
+// sequence_order); still accepted.
 constexpr uint32_t kPlanV1Size = offsetof(sa_attn_plan, order_n);
+constexpr uint32_t kPlanV2Size = offsetof(sa_attn_plan, tail_folded);
+bool plan_size_ok(uint32_t size) { return size == sizeof(sa_attn_plan) || size == kPlanV2Size || size == kPlanV1Size; }
 
 int num_cus();
 
@@ -875,7 +878,7 @@ const char* sa_attention_kernel_name(const sa_attn_args* args) {
 int sa_attention_plan(const sa_attn_args* args, sa_attn_plan* plan) {
   if (plan == nullptr) return fail(SA_ERR_INVALID, "plan is NULL");
   const uint32_t size = plan->struct_size;
-  if (size != sizeof(sa_attn_plan) && size != kPlanV1Size)
+  if (!plan_size_ok(size))
     return fail(SA_ERR_INVALID, "plan struct_size %u does not match sizeof(sa_attn_plan) = %zu", size,
                 sizeof(sa_attn_plan));
   sa::AttnParams p;
@@ -903,11 +906,13 @@ int sa_attention_plan(const sa_attn_args* args, sa_attn_plan* plan) {
     plan->workgroups = sa::flash_mfma_workgroups(p, c.nsplit, num_cus());
     const int64_t tail = sa::flash_mfma_tail_units(p, c.nsplit, num_cus());
     if (tail > 0) {
-      const bool small = sa::flash_mfma_tail_kernel(p, c.nsplit, num_cus()) == sa::TAIL_SMALL;
+      const int tk = sa::flash_mfma_tail_kernel(p, c.nsplit, num_cus());
+      const bool small = tk == sa::TAIL_SMALL;
       plan->tail_kernel = small ? SA_KERNEL_FLASH_SMALL : SA_KERNEL_FLASH;
       plan->tail_key_split = small ? sa::flash_small_waves(p) : 2;
       int64_t first = 0;
       plan->tail_workgroups = sa::flash_mfma_tail_groups(p, c.nsplit, num_cus(), &first);
+      plan->tail_folded = tk == sa::TAIL_FOLD ? 1 : 0;
     }
   } else if (c.path == Path::kSmall || c.path == Path::kSmall16) {
     const bool g16 = c.path == Path::kSmall16;
@@ -947,7 +952,7 @@ int32_t sa_attention_variant_count(void) {
 int sa_attention_variant(int32_t index, sa_attn_plan* plan) {
   if (plan == nullptr) return fail(SA_ERR_INVALID, "plan is NULL");
   const uint32_t size = plan->struct_size;
-  if (size != sizeof(sa_attn_plan) && size != kPlanV1Size)
+  if (!plan_size_ok(size))
     return fail(SA_ERR_INVALID, "plan struct_size %u does not match sizeof(sa_attn_plan) = %zu", size,
                 sizeof(sa_attn_plan));
   const int nflash = sa::flash_mfma_variants(nullptr, 0);

@@ -90,8 +90,24 @@ struct FlashOrder {
 };
 struct NoOrder {};
 
-template <int D, int NSPLIT, int BIAS, int MASK, typename Order>
-__device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord) {
+// The K/V staging area of one flash_body: [stage][K tile, V tile] of 32 * NSPLIT keys, two stages
+// (one for a folded piece, which shares the LDS of the kernel's first unit).
+template <int D, int NSPLIT, bool FOLD = false>
+constexpr int kLdsFloats = (FOLD ? 1 : 2) * 2 * 32 * NSPLIT * D;
+// Names the folded kernel's instantiations of flash_body, so that they have their own LDS array.
+template <int D>
+struct FoldTag {};
+
+// FOLD: the 64-query piece a workgroup of the folded launch runs after its own unit (2-way key
+// split, one LDS stage, no operand prefetch: it runs within the first unit's 128 VGPRs and 32 KiB,
+// staging its tiles in `lds_in`, the first unit's area, which that body passes out through
+// `lds_out`; tid_in is the thread id, opaque, so that the piece recomputes its lane addressing
+// instead of keeping the first unit's live). Tag names the folded kernel's instantiations, so that
+// they have LDS arrays of their own; the plain kernels' instantiations (Tag void) compile to the
+// code they had before the folded kernel existed.
+template <int D, int NSPLIT, int BIAS, int MASK, typename Order, bool FOLD = false, typename Tag = void>
+__device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord, const int tid_in = 0,
+                                           float* lds_in = nullptr, float** lds_out = nullptr) {
   constexpr int QG = 4 / NSPLIT;         // query groups (of 32) per workgroup
   constexpr int QT = 32 * QG;            // queries per workgroup
   constexpr int KT = 32 * NSPLIT;        // keys staged per step
@@ -103,9 +119,21 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
   static_assert(NI * 256 == KT * CPR, "tile must split evenly over 256 threads");
   constexpr int RB = QT + KT - 1;        // relative-bias entries needed per step
   constexpr int MSTRIDE = 16 * NDB + 2;  // merge record per lane: O tiles, m, l
-  static_assert((NSPLIT - 1) * QG * 64 * MSTRIDE <= 4 * TILE, "merge records must fit in the tiles");
+  constexpr int STAGES = FOLD ? 1 : 2;
+  static_assert(!FOLD || (NSPLIT == 2 && BIAS == BIAS_NONE && MASK == MASK_NONE), "only the plain split kernel folds");
+  static_assert((NSPLIT - 1) * QG * 64 * MSTRIDE <= STAGES * 2 * TILE, "merge records must fit in the tiles");
+  static_assert(kLdsFloats<D, NSPLIT, FOLD> == STAGES * 2 * TILE, "LDS staging size");
 
-  __shared__ __attribute__((aligned(16))) float lds[2 * 2 * TILE];  // [stage][K tile, V tile]
+  __shared__ __attribute__((aligned(16))) float lds[FOLD ? 1 : kLdsFloats<D, NSPLIT>];  // [stage][K tile, V tile]
+  if constexpr (!std::is_void<Tag>::value && !FOLD) *lds_out = lds;
+  auto lds_at = [&](int off) -> float* {
+    if constexpr (FOLD) {
+      return lds_in + off;
+    } else {
+      return lds + off;
+    }
+  };
+
   __shared__ float lds_rb[BIAS == BIAS_RELPOS ? 2 * RB : 1];         // [stage][relative bias]
   __shared__ float lds_km[MASK == MASK_KEY_MASK ? 2 * KT : 1];       // [stage][0 or -inf per key]
 
@@ -115,7 +143,7 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
   // cross-attention 39.6 -> 38.7 us; raised only after the unit decode it measured 40.6 us, and the
   // same boost on the self-attention launches cost them about 1 us)
   if constexpr (MASK == MASK_KEY_LEN_ORDERED) __builtin_amdgcn_s_setprio(3);
-  const int tid = threadIdx.x;
+  const int tid = FOLD ? tid_in : (int)threadIdx.x;
   const int lane = tid & 63;
   // wave-uniform in a scalar register, so per-block conditions compile to scalar branches
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -152,23 +180,31 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
   // Full steps address rows from a wave-uniform base plus per-lane 32-bit offsets; the step
   // holding the last valid key clamps rows past it to that key.
   auto chunk_of = [&](int n, int& row, int& ck, int& cv) {
-    const int pc_all = (n * 4 + wave) * 64 + lane;
+    int pc_all = (n * 4 + wave) * 64 + lane;
+    if constexpr (FOLD) {
+      // a folded piece recomputes its offsets at every copy (an opaque thread id: nothing to hoist)
+      int t = tid;
+      asm volatile("" : "+v"(t));
+      pc_all = n * 256 + t;
+    }
     row = pc_all / CPR;
     const int pc = pc_all % CPR;
     ck = 4 * (pc ^ (row & 15));
     cv = 4 * (pc ^ (((row >> 2) & 1) << 3));
   };
   unsigned koff[NI], voff[NI];  // byte offsets from the step's first row
+  if constexpr (!FOLD) {
 #pragma unroll
-  for (int n = 0; n < NI; ++n) {
-    int row, ck, cv;
-    chunk_of(n, row, ck, cv);
-    koff[n] = 4u * (unsigned)(row * (int)p.ldk + ck);
-    voff[n] = 4u * (unsigned)(row * (int)p.ldv + cv);
+    for (int n = 0; n < NI; ++n) {
+      int row, ck, cv;
+      chunk_of(n, row, ck, cv);
+      koff[n] = 4u * (unsigned)(row * (int)p.ldk + ck);
+      voff[n] = 4u * (unsigned)(row * (int)p.ldv + cv);
+    }
   }
   // rows past `lim` (the key length, or Lk for a speculative issue) re-read row lim - 1
   auto issue = [&](int step, int buf, int lim) {
-    float* kt = lds + buf * 2 * TILE;
+    float* kt = lds_at(buf * 2 * TILE);
     float* vt = kt + TILE;
     const int key0 = step * KT;
     if (key0 + KT <= lim) {
@@ -177,6 +213,13 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
 #pragma unroll
       for (int n = 0; n < NI; ++n) {
         const int blk64 = n * 4 + wave;  // 64-chunk (1 KiB) block of the tile
+        if constexpr (FOLD) {
+          // a folded piece recomputes its offsets at every copy rather than holding them
+          int row, ck, cv;
+          chunk_of(n, row, ck, cv);
+          koff[n] = 4u * (unsigned)(row * (int)p.ldk + ck);
+          voff[n] = 4u * (unsigned)(row * (int)p.ldv + cv);
+        }
         buffer_to_lds16(kr, koff[n], kt + blk64 * 256);
         buffer_to_lds16(vr, voff[n], vt + blk64 * 256);
       }
@@ -255,7 +298,7 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
     // kernels waiting for their second tile).
     if constexpr (kSpec) {
       if (p.Lk > KT) issue(1, 1, p.Lk);
-    } else if (nstep > 1) {
+    } else if (STAGES == 2 && nstep > 1) {
       issue(1, 1, kv_len);
     }
     if constexpr (MASK == MASK_KEY_LEN_ORDERED) __builtin_amdgcn_s_setprio(0);
@@ -280,17 +323,17 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
     // step 1 itself was issued before the loop) overwrites
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (step >= 1 && step + 1 < nstep) issue(step + 1, buf ^ 1, kv_len);
+    if (STAGES == 2 && step >= 1 && step + 1 < nstep) issue(step + 1, buf ^ 1, kv_len);
     const int blk = step * NSPLIT + ks;
     if (blk < nblk) {
       const int k0 = blk * 32;
-      const float* kt = lds + buf * 2 * TILE;
+      const float* kt = lds_at(buf * 2 * TILE);
       const float* vt = kt + TILE;
       // a speculatively issued tile holding the last valid key: its V rows past the key length are
       // zeroed (every thread its own chunks, rows pc / CPR) before the PV products read them
       const bool spec_fix = kSpec && step <= 1 && k0 + 32 > kv_len;
       if (spec_fix) {
-        float* vw = lds + buf * 2 * TILE + TILE;
+        float* vw = lds_at(buf * 2 * TILE + TILE);
 #pragma unroll
         for (int i = 0; i < KT * CPR / 256; ++i) {
           const int pc = tid + 256 * i;
@@ -304,7 +347,7 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
       // Key-split variants (head dim 64) run one or two waves per SIMD with registers to spare: all
       // K operands of the block are read before the MFMA chain, so it never waits on LDS (with 4
       // waves per SIMD the other waves hide those waits and the registers are not there).
-      constexpr bool kPrefetch = NSPLIT > 1 && D == 64;
+      constexpr bool kPrefetch = NSPLIT > 1 && D == 64 && !FOLD;
       f32x4 kpre[kPrefetch ? QREG / 4 : 1];
       if constexpr (kPrefetch) {
 #pragma unroll
@@ -351,7 +394,7 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
         }
       }
       // likewise the V operands of the PV step (head dim 64), read while the softmax runs
-      constexpr bool vPrefetch = NSPLIT > 1 && D == 64;
+      constexpr bool vPrefetch = NSPLIT > 1 && D == 64 && !FOLD;
       const float* vrow = vt + (ks * 32 + 4 * half) * D + col;
       float vpre[vPrefetch ? 16 * NDB : 1];
       if constexpr (vPrefetch) {
@@ -456,13 +499,22 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
     if (step < nstep) step_body(step, std::integral_constant<int, 0>{});
   } else {
     // the key-split kernels run one to a few steps: one copy of the body, stage chosen at run time
-    for (int step = 0; step < nstep; ++step) step_body(step, step & 1);
+    for (int step = 0; step < nstep; ++step) {
+      if constexpr (STAGES == 2) {
+        step_body(step, step & 1);
+      } else {
+        // one stage: the next tile goes in once every wave is done with this one
+        step_body(step, 0);
+        __syncthreads();
+        if (step + 1 < nstep) issue(step + 1, 0, kv_len);
+      }
+    }
   }
 
   // ---- merge the key splits: waves ks > 0 publish (O, m, l), wave ks == 0 combines
   if constexpr (NSPLIT > 1) {
     __syncthreads();  // every wave is done with the tiles the records overwrite
-    float* rec = lds + ((ks - 1) * QG + qg) * 64 * MSTRIDE + lane;
+    float* rec = lds_at(((ks - 1) * QG + qg) * 64 * MSTRIDE + lane);
     if (ks > 0) {
 #pragma unroll
       for (int t = 0; t < NDB; ++t)
@@ -476,7 +528,7 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
     float mt = m;
 #pragma unroll
     for (int sp = 1; sp < NSPLIT; ++sp) {
-      const float* o2 = lds + ((sp - 1) * QG + qg) * 64 * MSTRIDE + lane;
+      const float* o2 = lds_at(((sp - 1) * QG + qg) * 64 * MSTRIDE + lane);
       mt = fmaxf(mt, o2[(16 * NDB) * 64]);
     }
     const float a0 = fast_exp2(m - mt);
@@ -485,7 +537,7 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
     for (int t = 0; t < NDB; ++t) oacc[t] *= a0;
 #pragma unroll
     for (int sp = 1; sp < NSPLIT; ++sp) {
-      const float* o2 = lds + ((sp - 1) * QG + qg) * 64 * MSTRIDE + lane;
+      const float* o2 = lds_at(((sp - 1) * QG + qg) * 64 * MSTRIDE + lane);
       const float a = fast_exp2(o2[(16 * NDB) * 64] - mt);
       l = fmaf(o2[(16 * NDB + 1) * 64], a, l);
 #pragma unroll
@@ -504,7 +556,7 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord)
     // speculative tiles the loop never waited for (zero or one step) have landed before LDS is reused
     if constexpr (kSpec) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();  // every wave is done with the K/V tiles
-    float* ot = lds + wave * 32 * D;
+    float* ot = lds_at(wave * 32 * D);
 #pragma unroll
     for (int t = 0; t < NDB; ++t) {
 #pragma unroll
@@ -567,6 +619,27 @@ __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK>)) void
   flash_body<D, NSPLIT, BIAS, MASK>(p, NoOrder{});
 }
 
+// Folded launch of an unbiased, unmasked head-dim-64 call whose 128-query units exceed one round of
+// four workgroups per CU by at most half a round: one workgroup per unit of the round, and the
+// workgroups dispatched first (one per CU) each run one 64-query piece of the units left over (2-way
+// key split) after their own unit, so that every CU gets the same share of the leftover work and no
+// second launch waits for the first one to drain.
+template <int D>
+__global__ __launch_bounds__(256, 4) void flash_mfma_fold_kernel(FlashArgs p) {
+  static_assert(kLdsFloats<D, 2, true> <= kLdsFloats<D, 1>, "the folded piece reuses the unit's LDS");
+  float* lds = nullptr;
+  flash_body<D, 1, BIAS_NONE, MASK_NONE, NoOrder, false, FoldTag<D>>(p, NoOrder{}, threadIdx.x, nullptr, &lds);
+  if ((int)blockIdx.x < p.fold.count) {
+    FlashArgs f = p;
+    f.aux = p.fold.first;
+    f.tiles = p.fold.count;
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));  // opaque: the piece's lane addressing is recomputed, not kept live
+    __syncthreads();               // every wave has read its output rows back out of the LDS
+    flash_body<D, 2, BIAS_NONE, MASK_NONE, NoOrder, true, FoldTag<D>>(f, NoOrder{}, tid, lds);
+  }
+}
+
 template <int D, int NSPLIT, int BIAS>
 __global__ __launch_bounds__(256, (kMinBlocksPerCU<D, NSPLIT, BIAS, MASK_KEY_LEN_ORDERED>)) void flash_mfma_ordered_kernel(
     FlashArgs p, FlashOrder ord) {
@@ -608,7 +681,18 @@ hipError_t launch_split(const AttnParams& p, int num_cus, hipStream_t stream) {
   // the last units may go to the small-launch kernel: this launch covers units [0, n - tail)
   const int64_t tail = flash_mfma_tail_units(p, NSPLIT, num_cus);
   const dim3 grid((unsigned)(n - tail));
-  const FlashArgs a = flash_args(p, n - tail);
+  FlashArgs a = flash_args(p, n - tail);
+  if constexpr (D == 64 && NSPLIT == 1) {
+    if (tail > 0 && flash_mfma_tail_kernel(p, NSPLIT, num_cus) == TAIL_FOLD) {
+      int64_t first = 0;
+      const int64_t count = flash_mfma_tail_groups(p, NSPLIT, num_cus, &first);
+      a.aux = num_cus;  // start-up stagger period
+      a.fold.first = (int32_t)first;
+      a.fold.count = (int32_t)count;
+      hipLaunchKernelGGL((flash_mfma_fold_kernel<64>), grid, dim3(256), 0, stream, a);
+      return hipGetLastError();
+    }
+  }
   hipError_t e;
   switch (p.bias_mode) {
     case BIAS_NONE: e = launch_mask<D, NSPLIT, BIAS_NONE>(a, p, grid, num_cus, stream); break;
@@ -722,7 +806,10 @@ int64_t flash_mfma_tail_units(const AttnParams& p, int nsplit, int num_cus) {
 int flash_mfma_tail_kernel(const AttnParams& p, int nsplit, int num_cus) {
   const int64_t tail = flash_mfma_tail_units(p, nsplit, num_cus);
   if (tail == 0) return TAIL_NONE;
-  return 4 * tail <= num_cus ? TAIL_SMALL : TAIL_SPLIT2;
+  if (4 * tail <= num_cus) return TAIL_SMALL;
+  // one round plus the leftover: folded into the round's first workgroups
+  const int64_t tiles = (int64_t)p.B * p.H * ((p.Lq + 127) / 128);
+  return tiles < 8 * (int64_t)num_cus ? TAIL_FOLD : TAIL_SPLIT2;
 }
 
 int64_t flash_mfma_tail_groups(const AttnParams& p, int nsplit, int num_cus, int64_t* first) {

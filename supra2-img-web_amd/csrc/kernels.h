@@ -66,6 +66,9 @@ struct FlashArgs {
   union {
     const int32_t* lut;  // relative-position bucket LUT
     int64_t sbias;       // dense bias batch stride
+    struct {
+      int32_t first, count;  // folded launch: the 64-query units [first, first + count) left over
+    } fold;
   };
 };
 static_assert(sizeof(FlashArgs) == 112, "flash kernel arguments must stay within 112 bytes");
@@ -98,7 +101,7 @@ int flash_mfma_per_cu(const AttnParams& p, int nsplit);
 // Units (128-query tiles) of a flash launch that go to a second launch (0 = none), the kernel of
 // that launch, and the work items [*first, *first + count) it runs (returns count): 32-query groups
 // of flash_small, or 64-query units of the 2-way key-split flash kernel.
-constexpr int TAIL_NONE = 0, TAIL_SMALL = 1, TAIL_SPLIT2 = 2;
+constexpr int TAIL_NONE = 0, TAIL_SMALL = 1, TAIL_SPLIT2 = 2, TAIL_FOLD = 3;
 int64_t flash_mfma_tail_units(const AttnParams& p, int nsplit, int num_cus);
 int flash_mfma_tail_kernel(const AttnParams& p, int nsplit, int num_cus);
 int64_t flash_mfma_tail_groups(const AttnParams& p, int nsplit, int num_cus, int64_t* first);

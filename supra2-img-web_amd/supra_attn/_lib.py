@@ -184,6 +184,7 @@ class AttnPlan(ctypes.Structure):
         ("tail_workgroups", c_int64),
         ("order_n", c_int32),  # revision 2: the host sequence schedule of a scheduled flash call
         ("sequence_order", ctypes.c_uint8 * 256),
+        ("tail_folded", c_int32),  # revision 3: the units past the first round run inside it
     ]
 
     def __init__(self):

@@ -27,7 +27,7 @@ check("addon exports", function () {
     "bucketLut", "positionBias", "eventCreate", "eventRecord", "eventElapsed", "eventDestroy"].forEach(function (f) {
     assert.strictEqual(typeof native[f], "function", f);
   });
-  assert.strictEqual(native.version(), 4);
+  assert.strictEqual(native.version(), 5);
   assert.strictEqual(native.SA_BIAS_RELPOS, 2);
   assert.strictEqual(native.SA_MASK_KEY_MASK, 2);
 });

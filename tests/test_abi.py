@@ -48,7 +48,7 @@ def test_every_declared_symbol_is_exported_and_bound():
 
 def test_version_and_constants():
     lib = _lib.load()
-    assert lib.sa_version() == 4
+    assert lib.sa_version() == 5
     text = open(HEADER).read()
     text += open(os.path.join(ROOT, "include", "supra_linear.h")).read()
     weights = open(os.path.join(ROOT, "include", "supra_weights.h")).read()
@@ -110,24 +110,28 @@ def big(B, Lq=256, **over):
 SMALL, FLASH = _lib.SA_KERNEL_FLASH_SMALL, _lib.SA_KERNEL_FLASH
 
 
-@pytest.mark.parametrize("B,Lq,tail_units,tail_kernel,tail_split,tail_wg", [
-    (56, 256, 0, 0, 0, 0),          # 1008 units: one round on 256 CUs
-    (57, 256, 2, SMALL, 4, 8),      # 1026: a round of 1024, two left: 8 groups of 32 queries
-    (60, 256, 56, SMALL, 4, 224),   # 1080: 56 left, 224 groups
-    (61, 256, 74, FLASH, 2, 148),   # 1098: 74 left, 296 groups would not fit: 148 units of 64 queries
-    (64, 256, 128, FLASH, 2, 256),  # the batch-64 DiT call: 128 left, 256 units of 64 queries
-    (71, 256, 0, 0, 0, 0),          # 1278: 254 left would need more than one workgroup per CU: one launch
-    (114, 256, 4, SMALL, 4, 16),    # 2052: two whole rounds and four left
-    (57, 200, 2, SMALL, 4, 7),      # 7 groups of 32 per head: the tail is one whole head of 2 units
-    (61, 200, 74, FLASH, 2, 148),   # 4 units of 64 per head (the last one 8 queries)
+@pytest.mark.parametrize("B,Lq,tail_units,tail_kernel,tail_split,tail_wg,folded", [
+    (56, 256, 0, 0, 0, 0, 0),          # 1008 units: one round on 256 CUs
+    (57, 256, 2, SMALL, 4, 8, 0),      # 1026: a round of 1024, two left: 8 groups of 32 queries
+    (60, 256, 56, SMALL, 4, 224, 0),   # 1080: 56 left, 224 groups
+    (61, 256, 74, FLASH, 2, 148, 1),   # 1098: 74 left, 296 groups would not fit: 148 units of 64 queries,
+                                       # folded into the first 148 workgroups of the round
+    (64, 256, 128, FLASH, 2, 256, 1),  # the batch-64 DiT call: 128 left, 256 units of 64, one per CU, folded
+    (71, 256, 0, 0, 0, 0, 0),          # 1278: 254 left would need more than one workgroup per CU: one launch
+    (114, 256, 4, SMALL, 4, 16, 0),    # 2052: two whole rounds and four left
+    (118, 256, 76, FLASH, 2, 152, 0),  # 2124: two whole rounds and 76 left: a second launch, not folded
+    (57, 200, 2, SMALL, 4, 7, 0),      # 7 groups of 32 per head: the tail is one whole head of 2 units
+    (61, 200, 74, FLASH, 2, 148, 1),   # 4 units of 64 per head (the last one 8 queries)
 ])
-def test_plan_reports_the_tail_launch(B, Lq, tail_units, tail_kernel, tail_split, tail_wg):
+def test_plan_reports_the_tail_launch(B, Lq, tail_units, tail_kernel, tail_split, tail_wg, folded):
     """The batch-B, 9-head self-attention call on 256 CUs (the count without a device): the units past
-    the last whole round of 1024 go to a second launch when it runs them at one workgroup per CU."""
+    the last whole round of 1024 run at one workgroup per CU, in a second launch, or, after a single
+    round, as 64-query units folded into the round's first workgroups."""
     plan = _lib.plan(big(B, Lq))
     assert plan.kernel == _lib.SA_KERNEL_FLASH and plan.name == b"flash_mfma_d64"
     assert plan.workgroups == B * 9 * ((Lq + 127) // 128) - tail_units
     assert (plan.tail_kernel, plan.tail_key_split, plan.tail_workgroups) == (tail_kernel, tail_split, tail_wg)
+    assert plan.tail_folded == folded
 
 
 @pytest.mark.parametrize("over", [
@@ -137,8 +141,9 @@ def test_plan_reports_the_tail_launch(B, Lq, tail_units, tail_kernel, tail_split
     dict(mask_mode=1, key_len=FAKE + (3 << 36)),              # key lengths: the result may not depend on
 ])                                                            # whether the schedule's host copy comes along
 def test_no_tail_launch_outside_the_plain_variants(over):
-    plan = _lib.plan(big(60, **over))
-    assert plan.kernel == _lib.SA_KERNEL_FLASH and plan.tail_kernel == 0
+    for B in (60, 64):  # a small-launch tail, a folded one
+        plan = _lib.plan(big(B, **over))
+        assert plan.kernel == _lib.SA_KERNEL_FLASH and plan.tail_kernel == 0 and plan.tail_folded == 0
 
 
 def test_generic_kernel_for_row_strides_beyond_32bit_copy_offsets():

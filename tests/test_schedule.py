@@ -285,9 +285,11 @@ def test_schedule_follows_the_chosen_kernel():
     assert q.kernel == _lib.SA_KERNEL_FLASH_SMALL16 and q.order_n == 0
 
 
-def test_plan_revision_1_is_accepted_and_not_overrun():
-    """A revision-1 sa_attn_plan (ending at tail_workgroups) still works; nothing past it is written."""
-    v1 = _lib.AttnPlan.order_n.offset
+@pytest.mark.parametrize("field", ["order_n", "tail_folded"])
+def test_plan_revision_1_and_2_are_accepted_and_not_overrun(field):
+    """A revision-1 sa_attn_plan (ending at tail_workgroups) or revision-2 one (ending at
+    sequence_order) still works; nothing past it is written."""
+    v1 = getattr(_lib.AttnPlan, field).offset
     buf = (ctypes.c_uint8 * ctypes.sizeof(_lib.AttnPlan))(*([0xAB] * ctypes.sizeof(_lib.AttnPlan)))
     plan = _lib.AttnPlan.from_buffer(buf)
     plan.struct_size = v1

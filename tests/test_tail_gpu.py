@@ -1,8 +1,9 @@
-"""GPU parity of flash launches whose last round goes to a second launch: more units (128-query
-tiles) than the 4-per-CU kernel holds at once, with few enough left over for one workgroup per CU
-of the small-launch kernel (32-query groups) or of the 2-way key-split flash kernel (64-query units).
-The first launch covers the leading units, the second the rest; every
-output row is checked against the PyTorch fp32 CPU path and the float64 brute force (1e-5)."""
+"""GPU parity of flash launches whose last round holds few units: more units (128-query tiles) than
+the 4-per-CU kernel holds at once, with few enough left over for one workgroup per CU of the
+small-launch kernel (32-query groups) or of the 2-way key-split flash kernel (64-query units). The
+first launch covers the leading units; the rest go to a second launch, or, after a single round, run
+as 64-query units inside it, on its first workgroups after their own units. Every output row is
+checked against the PyTorch fp32 CPU path and the float64 brute force (1e-5)."""
 
 from __future__ import annotations
 
@@ -32,8 +33,9 @@ def tail_units(call) -> int:
     (60, 256, 256),   # 1080 units: a tail of 56 (224 small workgroups)
     (60, 250, 250),   # ragged
     (57, 200, 230),   # 7 groups of 32 per (b, h): the tail starts inside a head
-    (64, 256, 256),   # the batch-64 DiT call: 128 left, 2-way key-split flash kernel
-    (61, 200, 230),   # 74 left, split kernel, ragged 64-query units
+    (64, 256, 256),   # the batch-64 DiT call: 128 left, 2-way key-split units folded into the round
+    (61, 200, 230),   # 74 left, folded split units, ragged 64-query units
+    (118, 256, 250),  # two rounds and 76 left: a second launch of the split kernel
 ])
 def test_tail_launch_parity(dev, B, Lq, Lk):
     call = make_call(B=B, H=9, D=64, Lq=Lq, Lk=Lk, seed=B * 7 + Lq, packed=(Lq == Lk), name=f"tail_B{B}_q{Lq}_k{Lk}")
@@ -48,6 +50,8 @@ def test_tail_launch_parity(dev, B, Lq, Lk):
         small = 4 * n_tail <= 256
         assert (plan.tail_kernel, plan.tail_key_split) == ((_lib.SA_KERNEL_FLASH_SMALL, 4) if small
                                                            else (_lib.SA_KERNEL_FLASH, 2))
+        tiles = B * 9 * ((Lq + 127) // 128)
+        assert plan.tail_folded == (0 if small or tiles >= 2 * 1024 else 1)
         out = st.run()
     finally:
         st.release()
