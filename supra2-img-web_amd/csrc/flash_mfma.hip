@@ -102,12 +102,13 @@ struct FoldTag {};
 // split, one LDS stage, no operand prefetch: it runs within the first unit's 128 VGPRs and 32 KiB,
 // staging its tiles in `lds_in`, the first unit's area, which that body passes out through
 // `lds_out`; tid_in is the thread id, opaque, so that the piece recomputes its lane addressing
-// instead of keeping the first unit's live). Tag names the folded kernel's instantiations, so that
+// instead of keeping the first unit's live; piece, in [0, p.tiles), is the piece's index in place of
+// the block index). Tag names the folded kernel's instantiations, so that
 // they have LDS arrays of their own; the plain kernels' instantiations (Tag void) compile to the
 // code they had before the folded kernel existed.
 template <int D, int NSPLIT, int BIAS, int MASK, typename Order, bool FOLD = false, typename Tag = void>
 __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord, const int tid_in = 0,
-                                           float* lds_in = nullptr, float** lds_out = nullptr) {
+                                           float* lds_in = nullptr, float** lds_out = nullptr, const int piece = 0) {
   constexpr int QG = 4 / NSPLIT;         // query groups (of 32) per workgroup
   constexpr int QT = 32 * QG;            // queries per workgroup
   constexpr int KT = 32 * NSPLIT;        // keys staged per step
@@ -154,7 +155,7 @@ __device__ __forceinline__ void flash_body(const FlashArgs& p, const Order& ord,
 
   const int q_tiles = (p.Lq + QT - 1) / QT;
   // the key-split kernels also run the leftover units of a larger launch: aux is then the first unit
-  int tile = xcd_remap(blockIdx.x, p.tiles);
+  int tile = xcd_remap(FOLD ? piece : (int)blockIdx.x, p.tiles);
   if constexpr (NSPLIT > 1 && MASK != MASK_KEY_MASK) tile += p.aux;
   const int qtile = tile % q_tiles;
   tile /= q_tiles;
@@ -629,14 +630,15 @@ __global__ __launch_bounds__(256, 4) void flash_mfma_fold_kernel(FlashArgs p) {
   static_assert(kLdsFloats<D, 2, true> <= kLdsFloats<D, 1>, "the folded piece reuses the unit's LDS");
   float* lds = nullptr;
   flash_body<D, 1, BIAS_NONE, MASK_NONE, NoOrder, false, FoldTag<D>>(p, NoOrder{}, threadIdx.x, nullptr, &lds);
-  if ((int)blockIdx.x < p.fold.count) {
+  const int piece = blockIdx.x;  // the first workgroup of each CU: pieces [0, count)
+  if (piece < p.fold.count) {
     FlashArgs f = p;
     f.aux = p.fold.first;
     f.tiles = p.fold.count;
     int tid = threadIdx.x;
     asm volatile("" : "+v"(tid));  // opaque: the piece's lane addressing is recomputed, not kept live
     __syncthreads();               // every wave has read its output rows back out of the LDS
-    flash_body<D, 2, BIAS_NONE, MASK_NONE, NoOrder, true, FoldTag<D>>(f, NoOrder{}, tid, lds);
+    flash_body<D, 2, BIAS_NONE, MASK_NONE, NoOrder, true, FoldTag<D>>(f, NoOrder{}, tid, lds, nullptr, piece);
   }
 }
 
