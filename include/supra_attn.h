@@ -196,8 +196,8 @@ typedef struct sa_attn_plan {
   /* Revision 2 (appended: a revision-1 struct, which ends at tail_workgroups, is still accepted and
    * these fields are then not written). The host sequence schedule of a FLASH call whose
    * mask_variant is SA_MASK_VARIANT_KEY_LEN_SCHEDULED: sequence_order[r] is the sequence launched at
-   * rank r (r < B; when 8 divides B, L2 domain x takes the ranks [x*B/8, (x+1)*B/8)) and order_n is
-   * B; otherwise order_n is 0 and sequence_order all zero. */
+   * rank r (r < B; L2 domain x takes the ranks from x*B/8 on, rounded as the grid's tiles split, to
+   * the next domain's first) and order_n is B; otherwise order_n is 0 and sequence_order all zero. */
   int32_t order_n;
   uint8_t sequence_order[256];
   /* Revision 3 (appended: revision-1 and revision-2 structs are still accepted, without it). 1 when

@@ -122,7 +122,8 @@ int num_cus();
 // cross-attention after 81 calls; the DiT repeats its prompts in all 14 blocks of every step). The
 // whole search is capped at kSearchOps placements; a launch for which one pass over the pairs does
 // not fit takes the round-robin deal of the longest-first order, and a B that 8 does not divide
-// plain longest first. States are kept for the last kScheduleSlots length sets (a guidance caller
+// step 1 alone, over the rank ranges the remap gives each domain (batch 58 of the sweep's lengths:
+// 46.6 us for plain longest first, which put every long sequence in the first domains). States are kept for the last kScheduleSlots length sets (a guidance caller
 // alternates two), each behind its own mutex: callers with different key lengths never wait for one
 // another, and callers with the same lengths wait at most one step.
 constexpr int64_t kSearchOps = 1 << 19;
@@ -171,8 +172,8 @@ struct ScheduleState {
   int32_t len[sa::kMaxOrder];
   uint8_t order[sa::kMaxOrder];
   int nb[sa::kMaxOrder];
-  int per = 0;
-  int64_t sim_ops = 0;
+  int start[9] = {};  // domain x holds the ranks [start[x], start[x + 1])
+  int64_t sim_ops = 0;  // of the largest domain
   bool done = true;
   int x = 0, pass = 0, u = 0, v = 0;
   bool dom_started = false, improved = false;
@@ -203,34 +204,47 @@ void schedule_start(ScheduleState& st) {
     std::stable_sort(idx, idx + B, [&](int a, int b) { return st.nb[a] > st.nb[b]; });
   }
   st.done = true;
-  if (B % 8 != 0 || st.nb[idx[0]] == st.nb[idx[B - 1]]) {  // (all equal: the launch order, i.e. no schedule)
+  if (st.nb[idx[0]] == st.nb[idx[B - 1]]) {  // all equal: the launch order, i.e. no schedule
     for (int j = 0; j < B; ++j) st.order[j] = (uint8_t)idx[j];
     return;
   }
-  const int per = B / 8;
-  // Work of one simulation (workgroups, the later ones scanning C CUs) and of one pass over the
-  // pairs of every domain; without room for one pass, the round-robin deal.
-  const int64_t units = per * std::min<int64_t>(std::max<int64_t>(m.T, 1), 1 << 20);
+  // The remap gives L2 domain x the B*T/8 tiles (to within one) from tile lo_x = x*q + min(x, r) on
+  // (q, r = the tile count over 8 and its remainder), i.e. the ranks from about lo_x / T: domain x
+  // holds the ranks [start[x], start[x + 1]) with start[x] = lo_x / T rounded (x*B/8 when 8 divides B).
+  {
+    const int64_t T = std::max<int64_t>(m.T, 1), n = (int64_t)B * T, q = n / 8, r = n % 8;
+    for (int x = 0; x < 8; ++x) st.start[x] = (int)((x * q + std::min<int64_t>(x, r) + T / 2) / T);
+    st.start[8] = B;
+  }
+  int most = 0;
+  for (int x = 0; x < 8; ++x) most = std::max(most, st.start[x + 1] - st.start[x]);
+  // Work of one simulation of the largest domain (workgroups, the later ones scanning C CUs) and of
+  // one pass over its pairs in every domain; without room for one pass, 8 dividing B, the
+  // round-robin deal.
+  const int64_t units = most * std::min<int64_t>(std::max<int64_t>(m.T, 1), 1 << 20);
   const int64_t sim_ops = units + std::max<int64_t>(units - (int64_t)m.S * m.C, 0) * m.C;
-  const int64_t pairs = (int64_t)per * (per - 1) / 2;
-  if (pairs == 0 || m.C < 1 || m.C > 64 || m.T < 1 || m.T > (1 << 20) || 8 * pairs * sim_ops > kSearchOps) {
+  const int64_t pairs = (int64_t)most * (most - 1) / 2;
+  const bool search = !(pairs == 0 || m.C < 1 || m.C > 64 || m.T < 1 || m.T > (1 << 20) || 8 * pairs * sim_ops > kSearchOps);
+  if (!search && B % 8 == 0) {
+    const int per = B / 8;
     for (int j = 0; j < B; ++j) st.order[(j % 8) * per + j / 8] = (uint8_t)idx[j];
     return;
   }
+  // step 1: longest first, each sequence to the domain with the least work among those not yet full
   int64_t total[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   int count[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   for (int j = 0; j < B; ++j) {
     int best = 0;
     int64_t bv = INT64_MAX;
     for (int x = 0; x < 8; ++x) {  // branch-free: the least work among the domains not yet full
-      const bool take = count[x] < per && total[x] < bv;
+      const bool take = count[x] < st.start[x + 1] - st.start[x] && total[x] < bv;
       bv = take ? total[x] : bv;
       best = take ? x : best;
     }
-    st.order[best * per + count[best]++] = (uint8_t)idx[j];
+    st.order[st.start[best] + count[best]++] = (uint8_t)idx[j];
     total[best] += st.nb[idx[j]];
   }
-  st.per = per;
+  if (!search) return;
   st.sim_ops = sim_ops;
   st.done = false;
   st.x = 0;
@@ -240,9 +254,10 @@ void schedule_start(ScheduleState& st) {
 // Advances the search by at most `budget` simulated placements (one simulation always fits).
 void schedule_advance(ScheduleState& st, int64_t budget) {
   const int64_t domain_ops = kSearchOps / 8;
-  const int per = st.per, T = (int)st.m.T, C = st.m.C, S = st.m.S;
+  const int T = (int)st.m.T, C = st.m.C, S = st.m.S;
   while (!st.done && budget > 0) {
-    uint8_t* seq = st.order + st.x * per;  // longest first within the domain already
+    uint8_t* seq = st.order + st.start[st.x];  // longest first within the domain already
+    const int per = st.start[st.x + 1] - st.start[st.x];
     if (!st.dom_started) {
       st.mx = simulate_domain(seq, per, st.nb, T, C, S, &st.sq);
       st.spent = st.sim_ops;

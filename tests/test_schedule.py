@@ -62,16 +62,18 @@ def longest_first(key_len, Lk=128):
     return sorted(range(len(nb)), key=lambda i: -nb[i])  # Python's sort is stable
 
 
-def heaviest_cu(order, nb, units, C=CUS // 8, S=4):
+def heaviest_cu(order, nb, units, C=CUS // 8, S=4, start=None):
     """The dispatch model, per L2 domain: local workgroup j of the first residency (S per CU) on CU
-    j % C, each later one on the CU with the fewest key blocks so far; returns the heaviest CU's."""
+    j % C, each later one on the CU with the fewest key blocks so far; returns the heaviest CU's.
+    Domain x holds the ranks [start[x], start[x + 1]) (x*B/8 on when 8 divides B)."""
     B = len(order)
-    per = B // 8
+    if start is None:
+        start = [x * (B // 8) for x in range(8)] + [B]
     worst = 0
     for x in range(8):
         load = np.zeros(C, dtype=np.int64)
         j = 0
-        for r in range(x * per, (x + 1) * per):
+        for r in range(start[x], start[x + 1]):
             for _ in range(units):
                 c = j % C if j < S * C else int(np.argmin(load))
                 load[c] += nb[order[r]]
@@ -126,11 +128,49 @@ def test_searched_schedules(B):
     assert max(sums) - min(sums) <= int(nb.max())
 
 
+def domain_starts(B, T):
+    """First rank of each L2 domain: the remap gives domain x the tiles from x*q + min(x, r) on (q, r =
+    the B*T tiles over 8 and the remainder), i.e. the ranks from that tile over T, rounded."""
+    n = B * T
+    q, r = divmod(n, 8)
+    s = [(x * q + min(x, r) + T // 2) // T for x in range(8)]
+    return s + [B]
+
+
+@pytest.mark.parametrize("B", [9, 13, 58, 63, 100])
+def test_batches_not_divisible_by_8_are_dealt_over_the_domains(B):
+    """B not a multiple of 8: longest first, each sequence to the L2 domain with the least key blocks
+    so far among those whose rank range (as the remap splits the tiles) is not full; the search then
+    only swaps ranks within a domain, and never makes the model's heaviest CU heavier."""
+    rng = np.random.default_rng(B)
+    kl = rng.integers(1, 129, size=B)
+    if B == 58:
+        kl = workloads.sweep_key_lengths()[:58]
+    nb = blocks(kl)
+    start = domain_starts(B, 18)
+    want = [None] * B
+    total, count = [0] * 8, [0] * 8
+    for i in longest_first(kl):
+        x = min((x for x in range(8) if count[x] < start[x + 1] - start[x]), key=lambda x: (total[x], x))
+        want[start[x] + count[x]] = i
+        count[x] += 1
+        total[x] += int(nb[i])
+    first = plan_for(kl)  # a new length set: step 1 and one bounded search step
+    p = settled_plan(kl)
+    got = list(p.sequence_order[:B])
+    assert p.order_n == B and sorted(got) == list(range(B))
+    for x in range(8):
+        assert sorted(got[start[x]:start[x + 1]]) == sorted(want[start[x]:start[x + 1]])
+    assert heaviest_cu(got, nb, 18, start=start) <= heaviest_cu(want, nb, 18, start=start)
+    assert sorted(first.sequence_order[:B]) == list(range(B))
+    sums = [int(sum(nb[got[r]] for r in range(start[x], start[x + 1]))) for x in range(8)]
+    plain = longest_first(kl)
+    plain_sums = [int(sum(nb[plain[r]] for r in range(start[x], start[x + 1]))) for x in range(8)]
+    assert max(sums) - min(sums) <= int(nb.max()) and max(sums) <= max(plain_sums)
+
+
 def test_fallbacks_are_longest_first():
     rng = np.random.default_rng(7)
-    # B not a multiple of 8: plain longest first (stable)
-    kl = rng.integers(0, 129, size=13)
-    assert list(plan_for(kl).sequence_order[:13]) == longest_first(kl)
     # one sequence per domain: nothing to search, the round-robin deal is the longest-first order
     kl = rng.integers(0, 129, size=8)
     kl[0] = 1
