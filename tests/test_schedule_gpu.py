@@ -77,7 +77,7 @@ def test_schedule_is_bitwise_neutral(dev, name, call):
     assert e["finite"] and e["rel_l2"] <= TOL and e["max_rel"] <= TOL, e
 
 
-RANDOM_BATCHES = [8, 16, 40, 72, 96, 200, 256]
+RANDOM_BATCHES = [8, 16, 40, 57, 72, 96, 99, 200, 255, 256]
 
 
 @pytest.mark.parametrize("B", RANDOM_BATCHES)
@@ -85,8 +85,9 @@ def test_schedule_random_batches(dev, B):
     """The schedule over batch sizes that exercise every path of its construction (18 units of 128
     queries per sequence): one sequence per L2 domain (B = 8, no swaps), the bounded swap search
     (16-72), a search too large for its budget (the round-robin deal of the longest-first order,
-    96-256), with random lengths including zero and full ones: bit-identical to the launch-order run
-    and within the usual bar of the oracle."""
+    96-256), batches that 8 does not divide (57, 99: dealt over the domains' rank ranges and searched;
+    255: dealt, beyond the search budget), with random lengths including zero and full ones:
+    bit-identical to the launch-order run and within the usual bar of the oracle."""
     rng = np.random.default_rng(100 + B)
     key_len = rng.integers(0, 129, size=B).astype(np.int32)
     key_len[0], key_len[-1] = 0, 128
