@@ -11,6 +11,11 @@
 //   seeing every other key block) and their partial softmax states are merged in LDS at the end:
 //   launches of under ~2 waves per SIMD then still spread over many SIMDs. (Head-dim-64 launches of
 //   at most 256 query groups, such as the batch-2 DiT calls, take flash_small instead.)
+//   A launch of one round of four workgroups per CU plus at most half a round (the batch-64 DiT
+//   self-attention: 1152 units on 256 CUs) runs as one round whose first workgroups, one per CU, each
+//   take a 64-query NSPLIT = 2 piece of the units left over after their own unit
+//   (flash_mfma_fold_kernel): every CU carries the same work, and no second launch waits for the
+//   round to drain.
 //
 // Per 32-key block a wave computes the transposed score tile S^T = K Q^T with 32x32x2 fp32 MFMAs:
 //   A operand  K[key = lane%32][d], B operand Q^T[d][query = lane%32], the head dim split between
