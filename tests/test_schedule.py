@@ -20,6 +20,7 @@ import time
 
 import numpy as np
 import pytest
+from hypothesis import given, settings, strategies as hst
 
 from supra_attn import _lib, workloads
 
@@ -167,6 +168,34 @@ def test_batches_not_divisible_by_8_are_dealt_over_the_domains(B):
     plain = longest_first(kl)
     plain_sums = [int(sum(nb[plain[r]] for r in range(start[x], start[x + 1]))) for x in range(8)]
     assert max(sums) - min(sums) <= int(nb.max()) and max(sums) <= max(plain_sums)
+
+
+@settings(max_examples=60, deadline=None)
+@given(data=hst.data())
+def test_uneven_batches_property(data):
+    """Random batches that 8 does not divide, head counts and query lengths: the order is a
+    permutation, and every L2 domain's rank range holds exactly the sequences the deal gives it
+    (longest first to the least-loaded domain not yet full); the search only reorders within them."""
+    B = data.draw(hst.integers(9, 255).filter(lambda b: b % 8 != 0))
+    H = data.draw(hst.sampled_from([1, 2, 9, 12]))
+    Lq = data.draw(hst.sampled_from([128, 256]))
+    kl = np.asarray(data.draw(hst.lists(hst.integers(-20, 200), min_size=B, max_size=B)), dtype=np.int32)
+    p = plan_for(kl, H=H, Lq=Lq)
+    nb = blocks(kl)
+    if p.kernel != _lib.SA_KERNEL_FLASH or nb.min() == nb.max():
+        return  # no schedule: another kernel, or every sequence the same length (the launch order)
+    got = list(p.sequence_order[:B]) if p.order_n else list(range(B))  # order_n 0: the identity order
+    assert sorted(got) == list(range(B))
+    T = H * -(-Lq // (128 // p.key_split))
+    start = domain_starts(B, T)
+    total, count, want = [0] * 8, [0] * 8, [[] for _ in range(8)]
+    for i in longest_first(kl):
+        x = min((x for x in range(8) if count[x] < start[x + 1] - start[x]), key=lambda x: (total[x], x))
+        want[x].append(i)
+        count[x] += 1
+        total[x] += int(nb[i])
+    for x in range(8):
+        assert sorted(got[start[x]:start[x + 1]]) == sorted(want[x])
 
 
 def test_fallbacks_are_longest_first():
