@@ -128,8 +128,9 @@ int sa_attention_f32(const sa_attn_args* args, void* stream);
  * tight serving loops, harnesses that forbid hipMalloc. No counterpart in the reference.
  * args->workspace and workspace_bytes are ignored: the kernels that merge partial results across
  * workgroups use the library's own per-GPU scratch (a static device array of
- * SA_NOALLOC_SCRATCH_BYTES), and a call that needs more (sa_attention_workspace_bytes) fails with
- * SA_ERR_UNSUPPORTED before any launch. Nothing in the call allocates. The library looks up a
+ * SA_NOALLOC_SCRATCH_BYTES). The library plans those merges to fit it, so every call
+ * sa_attention_f32 takes runs here too; a call that would need more (sa_attention_workspace_bytes)
+ * would fail with SA_ERR_UNSUPPORTED before any launch. Nothing in the call allocates. The library looks up a
  * GPU's scratch address (hipGetSymbolAddress, which loads the library's device code on that GPU if
  * nothing has yet) once, at its first use on that GPU: sa_set_device, sa_malloc, sa_stream_create or
  * any operator call there. A caller that captures these calls into a HIP graph makes one of those

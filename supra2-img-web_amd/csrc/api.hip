@@ -674,6 +674,7 @@ namespace {
 // `scratch` names a host-side stand-in, never the device memory: host code uses only the address
 // hipGetSymbolAddress returns for the current device (kept per device in g_scratch).
 constexpr int64_t kScratchBytes = SA_NOALLOC_SCRATCH_BYTES;
+static_assert(kScratchBytes == sa::kWideMaxRecordBytes, "wide-head plans are sized to this scratch");
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 std::atomic<void*> g_scratch[kMaxDevices];
 

@@ -138,6 +138,9 @@ hipError_t launch_flash_small16(const AttnParams& p, hipStream_t stream);
 // split across the waves of a workgroup (D = 256) or score blocks dealt to them (D = 512), keys
 // split across workgroups, partials merged by a second kernel via a workspace.
 constexpr int kWideMaxChunks = 16;
+// Largest merge-record workspace a plan may ask for: the allocation-free entry point's per-GPU
+// scratch, so that entry point takes every wide-head call the workspace entry point takes.
+constexpr int64_t kWideMaxRecordBytes = int64_t(32) << 20;
 struct WidePlan {
   int q_groups;       // 32-query groups per (sequence, head)
   int nks;            // key chunks per group (workgroups sharing one query group)

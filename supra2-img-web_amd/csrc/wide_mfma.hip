@@ -872,22 +872,42 @@ int wide_mfma_variants(FlashVariant* out, int cap) {
   return n;
 }
 
+// Key chunks per query group: of the chunk counts up to kWideMaxChunks whose merge records fit
+// kWideMaxRecordBytes, the one with the shortest modelled makespan (ties: fewer chunks). A
+// workgroup costs the key blocks of its chunk plus about two blocks of start-up and stores; the
+// workgroups run in rounds of one per CU (D = 512: one wave per SIMD at 400 registers) or two
+// (D = 256: 80 KiB of LDS); a split adds the merge, about half a block plus one block per 22 MB of
+// records. One block is 32 queries x 32 keys over all head dims (about 4.4 us of a CU at
+// D = 512). For one head of 1024 tokens this is 8 chunks of 4 blocks (256 workgroups, one round);
+// for 2304 tokens 3 chunks of 24 blocks (216 workgroups) rather than 4 of 20 blocks, whose 288
+// workgroups would take two rounds.
 WidePlan wide_mfma_plan(const AttnParams& p, int num_cus) {
   WidePlan plan;
   plan.q_groups = (p.Lq + 31) / 32;
   const int64_t base = (int64_t)p.B * p.H * plan.q_groups;
-  // one workgroup per CU at D = 512 (one wave per SIMD at 400 registers), two at D = 256 (80 KiB LDS)
-  const int per_cu = p.D == 512 ? 1 : 2;
-  const int64_t target = (int64_t)num_cus * per_cu;
+  const int64_t target = (int64_t)num_cus * (p.D == 512 ? 1 : 2);
   const int nblk = (p.Lk + 31) / 32;
-  int nks = 1;
-  if (base < target) nks = (int)((target + base - 1) / base);
-  nks = std::max(1, std::min({nks, nblk, kWideMaxChunks}));
   // D = 512 takes keys in rounds of four blocks (wide_rows_kernel): chunks of whole rounds
   const int unit = p.D == 512 ? 4 : 1;
-  const int blocks_per_chunk = (nblk + nks * unit - 1) / (nks * unit) * unit;
-  plan.chunk = 32 * blocks_per_chunk;
-  plan.nks = (p.Lk + plan.chunk - 1) / plan.chunk;  // chunks that hold at least one key
+  const int64_t rec_bytes = (int64_t)(32 * p.D + 64) * (int64_t)sizeof(float);
+  double best = 0.0;
+  int best_bpc = 0, best_n = 0;
+  for (int want = 1; want <= kWideMaxChunks; ++want) {
+    const int bpc = (nblk + want * unit - 1) / (want * unit) * unit;
+    const int n = (nblk + bpc - 1) / bpc;  // chunks that hold at least one key
+    if (n == best_n) continue;
+    const double records = n > 1 ? (double)(base * n) * (double)rec_bytes : 0.0;
+    if (records > (double)kWideMaxRecordBytes) continue;
+    const double rounds = (double)((base * n + target - 1) / target);
+    const double cost = rounds * (bpc + 2) + (n > 1 ? 0.5 + records / 22e6 : 0.0);
+    if (best_n == 0 || cost < best) {
+      best = cost;
+      best_bpc = bpc;
+      best_n = n;
+    }
+  }
+  plan.chunk = 32 * best_bpc;
+  plan.nks = best_n;
   plan.ws_floats = plan.nks > 1 ? base * plan.nks * (int64_t)(32 * p.D + 64) : 0;
   return plan;
 }

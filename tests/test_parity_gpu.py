@@ -206,7 +206,9 @@ def test_generic_head_dims(dev, D):
                                           # D = 512 in several rounds of four key blocks per workgroup: one
                                           # chunk per query group (3 rounds, the last with one wave's block
                                           # and a partial one), and 10 chunks of 2 rounds, the last chunk short
-                                          (512, 8, 1, 1024, 300), (512, 1, 1, 64, 2500)])
+                                          (512, 8, 1, 1024, 300), (512, 1, 1, 64, 2500),
+                                          # 2304 tokens: 3 chunks of 768 keys (D = 512), 7 of 352 (D = 256)
+                                          (512, 1, 1, 2304, 2304), (256, 1, 1, 2304, 2304)])
 def test_wide_shapes(dev, D, B, H, Lq, Lk):
     call = make_call(B=B, H=H, D=D, Lq=Lq, Lk=Lk, seed=D + Lq + Lk)
     assert _lib.kernel_name(Staged(dev, call).args) == f"wide_mfma_d{D}"

@@ -4,6 +4,8 @@ loop steps for every splitting wave and ragged query and key lengths (sa_attenti
 from __future__ import annotations
 
 import pytest
+from hypothesis import given, settings
+from hypothesis import strategies as st
 
 from supra_attn import _lib
 from variant_cases import (SMALL, SMALL16, WIDE_SHAPES, call_for, fake_args, flash_variants, steps_per_wave,
@@ -78,3 +80,48 @@ def test_wide_cases_cover_split_and_unsplit():
         chunks.setdefault(v[1], set()).add(plan.key_chunks > 1)
     assert chunks == {256: {True, False}, 512: {True, False}}
     assert len(WIDE_SHAPES) == 6
+
+
+def wide_plan(B, H, D, Lq, Lk):
+    a = _lib.AttnArgs(B=B, H=H, D=D, Lq=Lq, Lk=Lk, q=0x7F0000000000, k=0x7F4000000000, v=0x7F8000000000,
+                      o=0x7FC000000000, ldq=H * D, ldk=H * D, ldv=H * D, sq=Lq * H * D, sk=Lk * H * D,
+                      sv=Lk * H * D, so=Lq * H * D, scale=D ** -0.5)
+    return _lib.plan(a)
+
+
+@pytest.mark.parametrize("D,B,H,L,chunks,keys", [
+    (512, 1, 1, 1024, 8, 128),    # the VAE call: 32 groups x 8 chunks of one round, 256 workgroups
+    (512, 2, 1, 1024, 4, 256),    # 64 groups x 4 chunks
+    (512, 1, 8, 1024, 1, 1024),   # 256 groups fill the CUs unsplit
+    (512, 1, 1, 2304, 3, 768),    # 216 workgroups in one round, not 4 chunks = 288 in two
+    (512, 1, 1, 1536, 4, 384),    # 192 workgroups of 12 blocks, not 6 chunks = 288 of 8 blocks
+    (512, 1, 1, 4096, 2, 2048),
+    (512, 1, 1, 5120, 3, 1792),   # two rounds of 56 blocks beat one round of 160 (1 chunk) or two of 80
+    (512, 1, 1, 9216, 1, 9216),   # 288 groups: any split would need more records than the scratch holds
+    (256, 1, 1, 1024, 16, 64),    # two workgroups per CU: 512 slots
+    (256, 1, 1, 2304, 7, 352),    # 504 workgroups, not 8 chunks = 576 in two rounds
+    (256, 1, 1, 16352, 1, 16352), # 511 groups fill the 512 slots unsplit (2 chunks: two rounds)
+])
+def test_wide_key_chunks_minimise_the_rounds(D, B, H, L, chunks, keys):
+    p = wide_plan(B, H, D, L, L)
+    assert (p.kernel, p.head_dim) == (_lib.SA_KERNEL_WIDE, D)
+    assert (p.key_chunks, p.keys_per_step) == (chunks, keys)
+    groups = B * H * ((L + 31) // 32)
+    assert p.workgroups == groups * chunks
+    rec = (32 * D + 64) * 4
+    assert p.workspace_bytes == (groups * chunks * rec if chunks > 1 else 0)
+
+
+@settings(max_examples=300, deadline=None)
+@given(D=st.sampled_from([256, 512]), B=st.integers(1, 4), H=st.integers(1, 16), Lq=st.integers(1, 20000),
+       Lk=st.integers(1, 20000))
+def test_every_wide_plan_fits_the_allocation_free_scratch(D, B, H, Lq, Lk):
+    """Whatever the shape, the key chunks cover the keys in whole rounds of the kernel, at most 16 of
+    them, and their merge records fit the allocation-free entry point's scratch (so that entry point
+    takes every wide-head call the workspace entry point takes)."""
+    p = wide_plan(B, H, D, Lq, Lk)
+    unit = 128 if D == 512 else 32
+    assert 1 <= p.key_chunks <= 16 and p.keys_per_step % unit == 0
+    assert p.key_chunks == -(-Lk // p.keys_per_step) and (p.key_chunks - 1) * p.keys_per_step < Lk
+    assert p.workspace_bytes <= _lib.SA_NOALLOC_SCRATCH_BYTES
+    assert (p.workspace_bytes > 0) == (p.key_chunks > 1)
