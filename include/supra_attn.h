@@ -190,7 +190,11 @@ typedef struct sa_attn_plan {
    * or of the flash kernel split by keys over 2 waves per 32 queries (SA_KERNEL_FLASH, 2), or, when
    * tail_folded is 1, as 64-query units of the latter run inside the first launch (see tail_folded);
    * tail_kernel is 0 when there are no such units, tail_workgroups the number of workgroups (or, folded,
-   * of 64-query units) they take. */
+   * of 64-query units) they take. WIDE calls whose query groups fill whole rounds of workgroups
+   * (one per CU at head dim 512, two at 256) and a few more: the whole rounds run unsplit (key_chunks
+   * 1, workgroups = their groups) and the groups past them follow in a second launch of the wide
+   * kernel (tail_kernel SA_KERNEL_WIDE), each split into tail_key_split key chunks merged after;
+   * tail_workgroups is that launch's grid. */
   int32_t tail_kernel;
   int32_t tail_key_split;
   int64_t tail_workgroups;

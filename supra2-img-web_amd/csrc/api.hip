@@ -941,9 +941,19 @@ int sa_attention_plan(const sa_attn_args* args, sa_attn_plan* plan) {
   } else if (c.path == Path::kWide) {
     plan->kernel = SA_KERNEL_WIDE;
     plan->head_dim = p.D;
-    plan->key_chunks = c.wide.nks;
-    plan->keys_per_step = c.wide.chunk;
-    plan->workgroups = (int64_t)p.B * p.H * c.wide.q_groups * c.wide.nks;
+    const int64_t groups = (int64_t)p.B * p.H * c.wide.q_groups;
+    if (c.wide.nks > 1 && c.wide.whole > 0) {  // whole rounds unsplit, then the rest in chunks
+      plan->key_chunks = 1;
+      plan->keys_per_step = c.wide.whole_chunk;
+      plan->workgroups = c.wide.whole;
+      plan->tail_kernel = SA_KERNEL_WIDE;
+      plan->tail_key_split = c.wide.nks;
+      plan->tail_workgroups = (groups - c.wide.whole) * c.wide.nks;
+    } else {
+      plan->key_chunks = c.wide.nks;
+      plan->keys_per_step = c.wide.chunk;
+      plan->workgroups = groups * c.wide.nks;
+    }
     plan->workspace_bytes = c.wide.ws_floats * (int64_t)sizeof(float);
   } else {
     plan->kernel = SA_KERNEL_GENERIC;

@@ -143,8 +143,11 @@ constexpr int kWideMaxChunks = 16;
 constexpr int64_t kWideMaxRecordBytes = int64_t(32) << 20;
 struct WidePlan {
   int q_groups;       // 32-query groups per (sequence, head)
-  int nks;            // key chunks per group (workgroups sharing one query group)
-  int chunk;          // keys per chunk (multiple of 32)
+  int nks;            // key chunks per split group (workgroups sharing one query group; 1: none split)
+  int chunk;          // keys per chunk of a split group (multiple of 32)
+  int whole_chunk;    // keys of an unsplit group's one chunk (all of them, in whole rounds of the kernel)
+  int64_t whole;      // with nks > 1: leading groups, in (sequence, head, group) order, that run
+                      // unsplit in a launch of their own before the split ones (0: every group split)
   int64_t ws_floats;  // workspace floats (0 when nks == 1)
 };
 bool wide_mfma_supported(const AttnParams& p);

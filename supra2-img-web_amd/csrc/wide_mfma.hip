@@ -61,7 +61,11 @@ struct WideArgs {
   float* o;
   const void* mask;   // key lengths (int32) | key mask (uint8)
   const float* bias;  // dense bias
-  int32_t sq, sk, sv, so;      // batch strides
+  int32_t sq, sk, sv;  // batch strides
+  union {
+    int32_t so;     // one key chunk: output batch stride
+    int32_t first;  // key chunks: the launch's first query group (its records start at the workspace)
+  };
   int32_t ldq, ldk, ldv, ldo;  // row strides
   int32_t Lq, Lk;
   int32_t sbias, smask;  // dense-bias and key-mask batch strides
@@ -72,11 +76,12 @@ struct WideArgs {
 };
 static_assert(sizeof(WideArgs) == 112, "wide kernel arguments must stay within 112 bytes");
 
-// Arguments of the merge kernel.
+// Arguments of the merge kernel: query groups [first, first + groups), whose records (nks each)
+// start at ws.
 struct MergeArgs {
   float* o;  // output + its element offset
   const float* ws;
-  int32_t B, H, Lq, so, ldo, q_groups, nks, nwg;
+  int32_t H, Lq, so, ldo, q_groups, nks, nwg, first, groups;
 };
 
 // Dense bias and key mask of one 32-key block in the 32x32 score layout, where lane (col, half)
@@ -176,7 +181,9 @@ __global__ __launch_bounds__(64 * NW, 1) void wide_mfma_kernel(WideArgs p) {
   const int q_groups = (p.Lq + 31) >> 5, nks = p.nks, chunk = p.chunk;
   int tile = xcd_remap(blockIdx.x, p.tiles);
   const int kc = tile % nks;
-  tile /= nks;
+  tile /= nks;                       // the launch's query group
+  const int slot_base = tile * nks;  // its chunks' records
+  if (nks > 1) tile += p.first;
   const int g = tile % q_groups;
   tile /= q_groups;
   const int h = tile % p.H;
@@ -184,7 +191,6 @@ __global__ __launch_bounds__(64 * NW, 1) void wide_mfma_kernel(WideArgs p) {
   const int q0 = g * 32;
   const int qi = q0 + col;
   const bool q_valid = qi < p.Lq;
-  const int slot_base = ((b * p.H + h) * q_groups + g) * nks;
 
   int kv_len = p.Lk;
   if constexpr (MASK == MASK_KEY_LEN) kv_len = min(max(static_cast<const int32_t*>(p.mask)[b], 0), p.Lk);
@@ -447,13 +453,14 @@ __global__ __launch_bounds__(256, 1) void wide_rows_kernel(WideArgs p) {
   const int q_groups = (p.Lq + 31) >> 5, nks = p.nks, chunk = p.chunk;
   int tile = xcd_remap(blockIdx.x, p.tiles);
   const int kc = tile % nks;
-  tile /= nks;
+  tile /= nks;                       // the launch's query group
+  const int slot_base = tile * nks;  // its chunks' records
+  if (nks > 1) tile += p.first;
   const int g = tile % q_groups;
   tile /= q_groups;
   const int h = tile % p.H;
   const int b = tile / p.H;
   const int q0 = g * 32;
-  const int slot_base = ((b * p.H + h) * q_groups + g) * nks;
 
   int kv_len = p.Lk;
   if constexpr (MASK == MASK_KEY_LEN) kv_len = min(max(static_cast<const int32_t*>(p.mask)[b], 0), p.Lk);
@@ -707,19 +714,20 @@ __global__ __launch_bounds__(256) void wide_merge_kernel(MergeArgs p) {
   // one XCD: consecutive merge workgroups (one query group's queries) run there and find the records
   // in that XCD's L2
   const int64_t idx = (int64_t)xcd_remap(blockIdx.x, p.nwg) * 256 + threadIdx.x;
-  const int64_t total = (int64_t)p.B * p.H * q_groups * 32 * C4;
+  const int64_t total = (int64_t)p.groups * 32 * C4;
   if (idx >= total) return;
   const int d4 = (int)(idx % C4);
   int64_t r = idx / C4;
   const int qq = (int)(r % 32);
-  r /= 32;  // (b*H + h)*q_groups + g
+  r /= 32;  // the launch's query group
+  const float* recs = p.ws + r * nks * REC;
+  r += p.first;  // (b*H + h)*q_groups + g
   const int g = (int)(r % q_groups);
   const int bh = (int)(r / q_groups);
   const int h = bh % p.H;
   const int b = bh / p.H;
   const int qi = g * 32 + qq;
   if (qi >= p.Lq) return;
-  const float* recs = p.ws + r * nks * REC;
   // One pass over the chunks in groups of 8 whose loads are all issued before any is used
   // (indexes clamped to the last chunk, surplus entries of a group skipped), with a running
   // maximum: the sums so far are rescaled when a group raises it. A query costs ceil(nks/8) load
@@ -797,20 +805,20 @@ bool fits32(int64_t x) { return x >= 0 && x <= 0x7fffffff; }
 
 template <int D>
 hipError_t launch_d(const AttnParams& p, const WidePlan& plan, float* ws, hipStream_t stream) {
-  const int64_t n = (int64_t)p.B * p.H * plan.q_groups * plan.nks;
-  if (n > 0x7fffffff) return hipErrorInvalidConfiguration;
+  const int64_t groups = (int64_t)p.B * p.H * plan.q_groups;
+  const int64_t whole = plan.nks > 1 ? plan.whole : groups;  // leading groups, unsplit
+  const int64_t split = groups - whole;                      // the rest, in nks chunks each
+  if (whole > 0x7fffffff || split * plan.nks > 0x7fffffff) return hipErrorInvalidConfiguration;
   WideArgs a;
   memset(&a, 0, sizeof a);
   a.q = p.q + p.q_off;
   a.k = p.k + p.k_off;
   a.v = p.v + p.v_off;
-  a.o = plan.nks > 1 ? ws : p.o + p.o_off;
   a.mask = p.mask_mode == MASK_KEY_LEN ? static_cast<const void*>(p.key_len) : static_cast<const void*>(p.key_mask);
   a.bias = p.bias;
   a.sq = (int32_t)p.sq;
   a.sk = (int32_t)p.sk;
   a.sv = (int32_t)p.sv;
-  a.so = (int32_t)p.so;
   a.ldq = (int32_t)p.ldq;
   a.ldk = (int32_t)p.ldk;
   a.ldv = (int32_t)p.ldv;
@@ -819,27 +827,35 @@ hipError_t launch_d(const AttnParams& p, const WidePlan& plan, float* ws, hipStr
   a.Lk = p.Lk;
   a.sbias = (int32_t)p.sbias;
   a.smask = (int32_t)p.smask;
-  a.tiles = (int32_t)n;
-  a.chunk = plan.chunk;
   a.scale_log2 = p.scale_log2;
   a.H = (int16_t)p.H;
-  a.nks = (int16_t)plan.nks;
-  const dim3 grid((unsigned)n);
-  hipError_t e;
-  if (p.bias_mode == BIAS_NONE)
-    e = launch_mask<D, BIAS_NONE>(a, p.mask_mode, grid, stream);
-  else if (p.bias_mode == BIAS_DENSE)
-    e = launch_mask<D, BIAS_DENSE>(a, p.mask_mode, grid, stream);
-  else
+  auto attend = [&](int64_t n) -> hipError_t {
+    a.tiles = (int32_t)n;
+    const dim3 grid((unsigned)n);
+    if (p.bias_mode == BIAS_NONE) return launch_mask<D, BIAS_NONE>(a, p.mask_mode, grid, stream);
+    if (p.bias_mode == BIAS_DENSE) return launch_mask<D, BIAS_DENSE>(a, p.mask_mode, grid, stream);
     return hipErrorInvalidValue;
-  if (e != hipSuccess || plan.nks == 1) return e;
-  const int64_t threads = (int64_t)p.B * p.H * plan.q_groups * 32 * (D / 4);
+  };
+  if (whole > 0) {
+    a.o = p.o + p.o_off;
+    a.so = (int32_t)p.so;
+    a.nks = 1;
+    a.chunk = plan.whole_chunk;
+    const hipError_t e = attend(whole);
+    if (e != hipSuccess || split == 0) return e;
+  }
+  a.o = ws;
+  a.first = (int32_t)whole;
+  a.nks = (int16_t)plan.nks;
+  a.chunk = plan.chunk;
+  const hipError_t e = attend(split * plan.nks);
+  if (e != hipSuccess) return e;
+  const int64_t threads = split * 32 * (D / 4);
   const int64_t blocks = (threads + 255) / 256;
   if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
   MergeArgs m;
   m.o = p.o + p.o_off;
   m.ws = ws;
-  m.B = p.B;
   m.H = p.H;
   m.Lq = p.Lq;
   m.so = (int32_t)p.so;
@@ -847,6 +863,8 @@ hipError_t launch_d(const AttnParams& p, const WidePlan& plan, float* ws, hipStr
   m.q_groups = plan.q_groups;
   m.nks = plan.nks;
   m.nwg = (int32_t)blocks;
+  m.first = (int32_t)whole;
+  m.groups = (int32_t)split;
   hipLaunchKernelGGL((wide_merge_kernel<D>), dim3((unsigned)blocks), dim3(256), 0, stream, m);
   return hipGetLastError();
 }
@@ -872,43 +890,53 @@ int wide_mfma_variants(FlashVariant* out, int cap) {
   return n;
 }
 
-// Key chunks per query group: of the chunk counts up to kWideMaxChunks whose merge records fit
-// kWideMaxRecordBytes, the one with the shortest modelled makespan (ties: fewer chunks). A
-// workgroup costs the key blocks of its chunk plus about two blocks of start-up and stores; the
-// workgroups run in rounds of one per CU (D = 512: one wave per SIMD at 400 registers) or two
-// (D = 256: 80 KiB of LDS); a split adds the merge, about half a block plus one block per 22 MB of
-// records. One block is 32 queries x 32 keys over all head dims (about 4.4 us of a CU at
-// D = 512). For one head of 1024 tokens this is 8 chunks of 4 blocks (256 workgroups, one round);
-// for 2304 tokens 3 chunks of 24 blocks (216 workgroups) rather than 4 of 20 blocks, whose 288
-// workgroups would take two rounds.
+// Key chunks per query group: of the plans whose merge records fit kWideMaxRecordBytes, the one
+// with the shortest modelled makespan (ties: the first found, fewer chunks). A workgroup costs the
+// key blocks of its chunk plus about two blocks of start-up and stores; workgroups run in rounds of
+// one per CU (D = 512: one wave per SIMD at 400 registers) or two (D = 256: 80 KiB of LDS); a split
+// adds the merge, about half a block plus one block per 22 MB of records. One block is 32 queries x
+// 32 keys over all head dims (about 4.4 us of a CU at D = 512). The plans: every group in the same
+// number of chunks (up to kWideMaxChunks), or, when the groups fill whole rounds and a few more,
+// the whole rounds unsplit and only the groups past them in chunks, in a second launch. For one
+// head of 1024 tokens this is 8 chunks of 4 blocks (256 workgroups, one round); for 2304 tokens 3
+// chunks of 24 blocks (216 workgroups) rather than 4 of 20 blocks, whose 288 workgroups would take
+// two rounds; for 9216 tokens (288 groups) 256 groups unsplit, then 32 groups in 8 chunks.
 WidePlan wide_mfma_plan(const AttnParams& p, int num_cus) {
   WidePlan plan;
   plan.q_groups = (p.Lq + 31) / 32;
   const int64_t base = (int64_t)p.B * p.H * plan.q_groups;
-  const int64_t target = (int64_t)num_cus * (p.D == 512 ? 1 : 2);
+  const int64_t slots = (int64_t)num_cus * (p.D == 512 ? 1 : 2);
   const int nblk = (p.Lk + 31) / 32;
   // D = 512 takes keys in rounds of four blocks (wide_rows_kernel): chunks of whole rounds
   const int unit = p.D == 512 ? 4 : 1;
   const int64_t rec_bytes = (int64_t)(32 * p.D + 64) * (int64_t)sizeof(float);
-  double best = 0.0;
-  int best_bpc = 0, best_n = 0;
-  for (int want = 1; want <= kWideMaxChunks; ++want) {
-    const int bpc = (nblk + want * unit - 1) / (want * unit) * unit;
-    const int n = (nblk + bpc - 1) / bpc;  // chunks that hold at least one key
-    if (n == best_n) continue;
-    const double records = n > 1 ? (double)(base * n) * (double)rec_bytes : 0.0;
-    if (records > (double)kWideMaxRecordBytes) continue;
-    const double rounds = (double)((base * n + target - 1) / target);
-    const double cost = rounds * (bpc + 2) + (n > 1 ? 0.5 + records / 22e6 : 0.0);
-    if (best_n == 0 || cost < best) {
-      best = cost;
-      best_bpc = bpc;
-      best_n = n;
+  auto rounds = [&](int64_t wgs) { return (double)((wgs + slots - 1) / slots); };
+  auto merge = [&](int64_t wgs) { return 0.5 + (double)(wgs * rec_bytes) / 22e6; };
+  auto fits = [&](int64_t wgs) { return wgs * rec_bytes <= kWideMaxRecordBytes; };
+  const int full = (nblk + unit - 1) / unit * unit;  // blocks of an unsplit group
+  double best = rounds(base) * (full + 2);
+  plan.nks = 1;
+  plan.chunk = plan.whole_chunk = 32 * full;
+  plan.whole = 0;
+  // split groups: `split` of them (the last ones) in n chunks of bpc blocks, after `whole` unsplit
+  auto consider = [&](int64_t whole, int64_t split) {
+    for (int want = 2; want <= kWideMaxChunks; ++want) {
+      const int bpc = (nblk + want * unit - 1) / (want * unit) * unit;
+      const int n = (nblk + bpc - 1) / bpc;  // chunks that hold at least one key
+      if (n == 1 || !fits(split * n)) continue;
+      const double cost = (whole > 0 ? rounds(whole) * (full + 2) : 0.0) + rounds(split * n) * (bpc + 2) +
+                          merge(split * n);
+      if (cost < best) {
+        best = cost;
+        plan.nks = n;
+        plan.chunk = 32 * bpc;
+        plan.whole = whole;
+      }
     }
-  }
-  plan.chunk = 32 * best_bpc;
-  plan.nks = best_n;
-  plan.ws_floats = plan.nks > 1 ? base * plan.nks * (int64_t)(32 * p.D + 64) : 0;
+  };
+  consider(0, base);
+  if (base > slots && base % slots != 0 && base <= 0x7fffffff) consider(base / slots * slots, base % slots);
+  plan.ws_floats = plan.nks > 1 ? (base - plan.whole) * plan.nks * (int64_t)(32 * p.D + 64) : 0;
   return plan;
 }
 

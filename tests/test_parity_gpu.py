@@ -14,6 +14,7 @@ from oracle import attention as orc
 from supra_attn import _lib, workloads
 from supra_attn.runner import Staged
 from cases import make_call
+from variant_cases import fake_args
 
 pytestmark = pytest.mark.gpu
 
@@ -208,11 +209,28 @@ def test_generic_head_dims(dev, D):
                                           # and a partial one), and 10 chunks of 2 rounds, the last chunk short
                                           (512, 8, 1, 1024, 300), (512, 1, 1, 64, 2500),
                                           # 2304 tokens: 3 chunks of 768 keys (D = 512), 7 of 352 (D = 256)
-                                          (512, 1, 1, 2304, 2304), (256, 1, 1, 2304, 2304)])
+                                          (512, 1, 1, 2304, 2304), (256, 1, 1, 2304, 2304),
+                                          # groups past whole rounds split alone: 256 + 32 in 8 chunks
+                                          # (D = 512), 512 + 32 in 16 chunks, ragged (D = 256)
+                                          (512, 1, 9, 1024, 1024), (256, 1, 17, 1000, 1000)])
 def test_wide_shapes(dev, D, B, H, Lq, Lk):
     call = make_call(B=B, H=H, D=D, Lq=Lq, Lk=Lk, seed=D + Lq + Lk)
     assert _lib.kernel_name(Staged(dev, call).args) == f"wide_mfma_d{D}"
     run_checked(dev, call, check_fp64=Lq * Lk < 500000)
+
+
+@pytest.mark.parametrize("bias_mode,mask_mode", [(_lib.SA_BIAS_NONE, _lib.SA_MASK_KEY_LEN),
+                                                 (_lib.SA_BIAS_DENSE, _lib.SA_MASK_KEY_MASK)])
+def test_wide_whole_rounds_then_split_groups(dev, bias_mode, mask_mode):
+    """288 query groups (2 sequences x 9 heads x 500 queries, D = 512): the first 256 run unsplit,
+    the last 32 (two heads of the second sequence) in key chunks, with key lengths or a key mask
+    and a dense bias per sequence."""
+    call = make_call(B=2, H=9, D=512, Lq=500, Lk=512, bias_mode=bias_mode, mask_mode=mask_mode,
+                     key_len=[512, 300] if mask_mode == _lib.SA_MASK_KEY_LEN else None, dense_bias_batched=True,
+                     seed=77 + mask_mode)
+    p = _lib.plan(fake_args(call, False))
+    assert (p.workgroups, p.tail_kernel, p.tail_workgroups) == (256, _lib.SA_KERNEL_WIDE, 32 * p.tail_key_split)
+    run_checked(dev, call, check_fp64=False)
 
 
 def test_wide_key_len_and_workspace_reuse(dev):

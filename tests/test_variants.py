@@ -97,19 +97,39 @@ def wide_plan(B, H, D, Lq, Lk):
     (512, 1, 1, 1536, 4, 384),    # 192 workgroups of 12 blocks, not 6 chunks = 288 of 8 blocks
     (512, 1, 1, 4096, 2, 2048),
     (512, 1, 1, 5120, 3, 1792),   # two rounds of 56 blocks beat one round of 160 (1 chunk) or two of 80
-    (512, 1, 1, 9216, 1, 9216),   # 288 groups: any split would need more records than the scratch holds
     (256, 1, 1, 1024, 16, 64),    # two workgroups per CU: 512 slots
     (256, 1, 1, 2304, 7, 352),    # 504 workgroups, not 8 chunks = 576 in two rounds
+    (256, 1, 1, 9216, 3, 3072),   # 864 workgroups of 96 blocks in two rounds
     (256, 1, 1, 16352, 1, 16352), # 511 groups fill the 512 slots unsplit (2 chunks: two rounds)
 ])
 def test_wide_key_chunks_minimise_the_rounds(D, B, H, L, chunks, keys):
     p = wide_plan(B, H, D, L, L)
     assert (p.kernel, p.head_dim) == (_lib.SA_KERNEL_WIDE, D)
-    assert (p.key_chunks, p.keys_per_step) == (chunks, keys)
+    assert (p.key_chunks, p.keys_per_step, p.tail_kernel) == (chunks, keys, 0)
     groups = B * H * ((L + 31) // 32)
     assert p.workgroups == groups * chunks
     rec = (32 * D + 64) * 4
     assert p.workspace_bytes == (groups * chunks * rec if chunks > 1 else 0)
+
+
+@pytest.mark.parametrize("D,B,H,L,whole,tail_chunks", [
+    (512, 1, 1, 9216, 256, 8),    # 288 groups: 256 unsplit, then 32 in 8 chunks of 36 blocks
+    (512, 1, 9, 1024, 256, 8),    # 9 heads of the VAE size: 288 groups likewise, chunks of 4 blocks
+    (512, 1, 1, 8448, 256, 14),   # 8 groups past the round, 14 chunks of 20 blocks
+    (512, 2, 9, 512, 256, 4),     # the 32 groups past the round span two heads of the second sequence
+    (256, 1, 17, 1024, 512, 16),  # 544 groups for 512 slots
+])
+def test_wide_groups_past_whole_rounds_are_split_alone(D, B, H, L, whole, tail_chunks):
+    """Groups that fill whole rounds and a few more: the whole rounds run unsplit (the main
+    launch) and only the groups past them are split into key chunks (a second launch and the
+    merge), instead of a second round of whole groups."""
+    p = wide_plan(B, H, D, L, L)
+    groups = B * H * ((L + 31) // 32)
+    unit = 128 if D == 512 else 32
+    assert (p.kernel, p.key_chunks, p.keys_per_step) == (_lib.SA_KERNEL_WIDE, 1, -(-L // unit) * unit)
+    assert p.workgroups == whole and (p.tail_kernel, p.tail_key_split) == (_lib.SA_KERNEL_WIDE, tail_chunks)
+    assert p.tail_workgroups == (groups - whole) * tail_chunks
+    assert p.workspace_bytes == (groups - whole) * tail_chunks * (32 * D + 64) * 4
 
 
 @settings(max_examples=300, deadline=None)
@@ -117,11 +137,21 @@ def test_wide_key_chunks_minimise_the_rounds(D, B, H, L, chunks, keys):
        Lk=st.integers(1, 20000))
 def test_every_wide_plan_fits_the_allocation_free_scratch(D, B, H, Lq, Lk):
     """Whatever the shape, the key chunks cover the keys in whole rounds of the kernel, at most 16 of
-    them, and their merge records fit the allocation-free entry point's scratch (so that entry point
-    takes every wide-head call the workspace entry point takes)."""
+    them, the launches cover every query group once, and the merge records fit the allocation-free
+    entry point's scratch (so that entry point takes every wide-head call the workspace entry point
+    takes)."""
     p = wide_plan(B, H, D, Lq, Lk)
     unit = 128 if D == 512 else 32
+    groups = B * H * ((Lq + 31) // 32)
     assert 1 <= p.key_chunks <= 16 and p.keys_per_step % unit == 0
     assert p.key_chunks == -(-Lk // p.keys_per_step) and (p.key_chunks - 1) * p.keys_per_step < Lk
     assert p.workspace_bytes <= _lib.SA_NOALLOC_SCRATCH_BYTES
-    assert (p.workspace_bytes > 0) == (p.key_chunks > 1)
+    if p.tail_kernel:  # whole rounds of unsplit groups, then the groups past them in chunks
+        slots = 256 if D == 512 else 512
+        assert p.tail_kernel == _lib.SA_KERNEL_WIDE and p.key_chunks == 1 and 2 <= p.tail_key_split <= 16
+        assert p.workgroups == groups // slots * slots and 0 < groups - p.workgroups < slots
+        assert p.tail_workgroups == (groups - p.workgroups) * p.tail_key_split
+        assert p.workspace_bytes == p.tail_workgroups * (32 * D + 64) * 4
+    else:
+        assert p.workgroups == groups * p.key_chunks
+        assert (p.workspace_bytes > 0) == (p.key_chunks > 1)

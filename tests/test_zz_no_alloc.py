@@ -65,6 +65,12 @@ def test_noalloc_matches_the_workspace_call_twice_then_smaller(dev):
                               seed=42))
 
 
+def test_noalloc_whole_rounds_then_split_groups(dev):
+    # 9 heads of the VAE size: 256 query groups unsplit, then 32 in 8 key chunks through the scratch
+    need = check_case(dev, make_call(B=1, H=9, D=512, Lq=1024, Lk=1024, seed=9))
+    assert need == 32 * 8 * (32 * 512 + 64) * 4
+
+
 def test_noalloc_flash_call_needs_no_scratch(dev):
     need = check_case(dev, workloads.dit_self(B=2, seed=0))
     assert need == 0
