@@ -138,8 +138,40 @@ def _wide_and_packed_cases(seed: int, n: int) -> list[dict]:
     return cases
 
 
+def _wide_round_cases(seed: int, n: int) -> list[dict]:
+    """Wide-head calls whose query groups fill one round of workgroups (256 at head dim 512, 512 at
+    256) and part of another: the plan runs the whole round unsplit and splits the groups past it
+    into key chunks, or splits every group alike. Ragged Lq and Lk, dense biases, both mask kinds."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        D = int(rng.choice([256, 512]))
+        slots = 256 if D == 512 else 512
+        B, H = int(rng.integers(1, 4)), int(rng.integers(1, 10))
+        per = -(-slots // (B * H))  # 32-query groups per (sequence, head) that just pass one round
+        Lq = 32 * int(rng.integers(per, per + max(2, per // 4) + 1)) - int(rng.integers(0, 32))
+        Lq = max(Lq, 32 * (per - 1) + 1)
+        Lk = int(rng.integers(33, 400))
+        kw = dict(B=B, H=H, D=D, Lq=Lq, Lk=Lk, seed=4000 + i, o_off=int(rng.choice([0, 8])),
+                  pad_cols=int(rng.choice([0, 4])))
+        if rng.random() < 0.5:
+            kw["bias_mode"] = _lib.SA_BIAS_DENSE
+            kw["dense_bias_batched"] = bool(rng.random() < 0.5)
+        r = rng.random()
+        if r < 0.4:
+            kw["mask_mode"] = _lib.SA_MASK_KEY_LEN
+            kw["key_len"] = [int(x) for x in rng.integers(0, Lk + 1, size=B)]
+        elif r < 0.8:
+            kw["mask_mode"] = _lib.SA_MASK_KEY_MASK
+            kw["key_mask_p"] = float(rng.choice([0.1, 0.5, 0.9]))
+        kw["name"] = (f"rand_wr{i}_B{B}H{H}D{D}q{Lq}k{Lk}_b{kw.get('bias_mode', 0)}m{kw.get('mask_mode', 0)}")
+        cases.append(kw)
+    return cases
+
+
 ATTENTION = _attention_cases(seed=2026, n=40)
 WIDE_PACKED = _wide_and_packed_cases(seed=2028, n=24)
+WIDE_ROUNDS = _wide_round_cases(seed=2029, n=8)
 LINEAR = _linear_cases(seed=2027, n=24)
 
 
@@ -193,6 +225,32 @@ def test_wide_and_packed_draw_reaches_its_variants():
     assert {(d, _lib.SA_BIAS_DENSE, _lib.SA_MASK_KEY_MASK) for d in (256, 512)} & wide, wide
     packed = [v for v in variants if v[0] == _lib.SA_KERNEL_FLASH_SMALL16 and v[4] == 3]
     assert len({v[3] for v in packed}) >= 2, variants
+
+
+@pytest.mark.parametrize("case", WIDE_ROUNDS, ids=[c["name"] for c in WIDE_ROUNDS])
+def test_random_wide_past_one_round(dev, case):
+    kw = dict(case)
+    key_len = kw.pop("key_len", None)
+    run_attention(dev, make_call(key_len=key_len, **kw), check_fp64=False)
+
+
+def test_wide_round_draw_reaches_split_tails():
+    """The third draw reaches plans that split only the groups past the whole round, at both head
+    dims, with a dense bias, key lengths and a key mask among them (host only)."""
+    from variant_cases import fake_args
+
+    tails = []
+    for case in WIDE_ROUNDS:
+        kw = dict(case)
+        key_len = kw.pop("key_len", None)
+        call = make_call(key_len=key_len, **kw)
+        p = _lib.plan(fake_args(call, False))
+        assert p.kernel == _lib.SA_KERNEL_WIDE, call.name
+        if p.tail_kernel == _lib.SA_KERNEL_WIDE:
+            tails.append((call.D, call.bias_mode, call.mask_mode))
+    assert {d for d, _, _ in tails} == {256, 512}, tails
+    assert {m for _, _, m in tails} >= {_lib.SA_MASK_KEY_LEN, _lib.SA_MASK_KEY_MASK}, tails
+    assert any(b == _lib.SA_BIAS_DENSE for _, b, _ in tails), tails
 
 
 @pytest.mark.parametrize("case", LINEAR, ids=[c["name"] for c in LINEAR])
