@@ -66,3 +66,46 @@ def test_tail_launch_parity(dev, B, Lq, Lk):
                     ld=ldo, sb=call.args.get("so", 0))
     written[idx.reshape(-1)] = True
     assert (out.reshape(-1)[~written] == SENTINEL).all()
+
+
+def _fold_draw(seed: int, n: int) -> list[dict]:
+    """Seeded calls whose units fill one round and part of a second that folds into it (more than 64
+    and at most 128 of them past the 1024 slots): any batch, head count and ragged lengths, packed or
+    separate q/k/v, padded rows and element offsets."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        B, H = int(rng.integers(1, 130)), int(rng.integers(1, 17))
+        Lq, Lk = int(rng.integers(129, 700)), int(rng.integers(33, 400))
+        tiles = B * H * ((Lq + 127) // 128)
+        if not 1024 + 64 < tiles <= 1024 + 128 or B * H * Lq * Lk > 60_000_000:
+            continue
+        out.append(dict(B=B, H=H, D=64, Lq=Lq, Lk=Lk, seed=5000 + len(out), packed=bool(rng.random() < 0.5),
+                        pad_cols=int(rng.choice([0, 4, 8])), q_off=int(rng.choice([0, 4, 12])),
+                        o_off=int(rng.choice([0, 8])), ldo_pad=int(rng.choice([0, 4])),
+                        name=f"fold_B{B}H{H}q{Lq}k{Lk}"))
+    return out
+
+
+FOLD_DRAW = _fold_draw(seed=2031, n=6)
+
+
+@pytest.mark.parametrize("case", FOLD_DRAW, ids=[c["name"] for c in FOLD_DRAW])
+def test_folded_launch_random_shapes(dev, case):
+    call = make_call(**case)
+    print(f"[case] {call.name}", flush=True)
+    st = Staged(dev, call, out_fill=SENTINEL)
+    try:
+        plan = _lib.plan(st.args)
+        assert (plan.kernel, plan.tail_folded) == (_lib.SA_KERNEL_FLASH, 1), call.name
+        out = st.run()
+    finally:
+        st.release()
+    e = orc.errors(orc.output_view(out, call), orc.reference_torch(call))
+    assert e["finite"] and e["rel_l2"] <= TOL and e["max_rel"] <= TOL, f"{call.name}: {e}"
+    ldo = call.args.get("ldo", 0) or call.H * call.D
+    written = np.zeros(out.size, dtype=bool)
+    idx = orc.heads(np.arange(out.size), B=call.B, L=call.Lq, H=call.H, D=call.D, off=call.args.get("o_off", 0),
+                    ld=ldo, sb=call.args.get("so", 0))
+    written[idx.reshape(-1)] = True
+    assert (out.reshape(-1)[~written] == SENTINEL).all()
